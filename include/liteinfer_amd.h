@@ -1,0 +1,152 @@
+/*
+ * liteinfer_amd — C ABI of the MI355X (gfx950) paged-attention library.
+ *
+ * The library holds the three device kernels that liteinfer's
+ * `attn_implementation="paged"` path runs, written in HIP for CDNA4:
+ *
+ *   li_kv_scatter      KV slot-write: this pass's K/V rows into pool slots.
+ *   li_paged_decode    one query per sequence over its paged context.
+ *   li_paged_prefill   packed / chunked queries, causal within the chunk,
+ *                      over a cached prefix.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers; strides are in ELEMENTS, not bytes.
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream).
+ *   - Nothing is allocated: outputs and workspaces belong to the caller.
+ *   - Nothing is read back to the host and nothing synchronises, so every
+ *     call can be captured into a hipGraph. Grids are sized from the host
+ *     integers passed in, never from device data.
+ *   - Return 0 on success, a negative LI_E* code otherwise; the message of
+ *     the last failure on the calling thread is li_last_error_string().
+ *   - Pool layout (liteinfer/cache/block_pool.py:63): one layer's K (and V)
+ *     store is [num_slots, num_kv_heads, head_dim] with the last axis
+ *     contiguous; slot s of block b holding token t is b*block_size + t.
+ *   - slot_table is [batch, max_context] int64, left-aligned; a row's columns
+ *     at or past its context length are never read
+ *     (liteinfer/cache/block_pool.py:135-148).
+ */
+#ifndef LITEINFER_AMD_H
+#define LITEINFER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of q / pools / out. */
+enum li_dtype { LI_F32 = 0, LI_F16 = 1, LI_BF16 = 2 };
+
+/* Error codes. */
+enum li_status {
+  LI_OK = 0,
+  LI_EINVAL = -1,       /* an argument is out of range or inconsistent */
+  LI_EUNSUPPORTED = -2, /* a shape or layout this build does not serve */
+  LI_ELAUNCH = -3,      /* the HIP runtime refused the launch */
+  LI_EWORKSPACE = -4    /* the workspace passed is too small */
+};
+
+/* Flags for li_paged_decode / li_paged_prefill. */
+enum li_flags {
+  LI_FLAG_NONE = 0,
+  LI_FLAG_FORCE_GENERIC = 1 /* run the general-shape kernel even where the
+                               MFMA kernel applies (used by the parity tests) */
+};
+
+/* Message of the last failure on this thread ("" if none). */
+const char* li_last_error_string(void);
+
+/* Version of this ABI; bumped whenever a signature changes. */
+int li_abi_version(void);
+
+/*
+ * KV slot-write. Replaces KVCache.scatter (liteinfer/cache/kv_cache.py:236-247)
+ * together with _tokens_first (kv_cache.py:250-253):
+ *     keys[slots.reshape(-1)]   = k.permute(0, 2, 1, 3).reshape(B*T, H, D)
+ *     values[slots.reshape(-1)] = v.permute(0, 2, 1, 3).reshape(B*T, H, D)
+ * k and v are [batch, num_kv_heads, tokens, head_dim] with arbitrary element
+ * strides (k_strides / v_strides = {batch, head, token, dim}); slots holds
+ * batch*tokens entries in batch-major token order. A bit-exact copy. A slot
+ * outside [0, num_slots) is not written (torch's index_put_ would raise).
+ */
+int li_kv_scatter(const void* k, const void* v, const int64_t* k_strides,
+                  const int64_t* v_strides, int64_t batch, int64_t tokens,
+                  const int64_t* slots, void* key_pool, void* value_pool,
+                  int64_t num_slots, int64_t pool_stride_slot,
+                  int64_t pool_stride_head, int num_kv_heads, int head_dim,
+                  int dtype, void* stream);
+
+/*
+ * How many partitions each sequence's key loop is cut into for a decode step
+ * of `batch` rows over a slot table `max_context` wide, on a device of
+ * `num_cus` compute units (0 = ask the current device). Counterpart of
+ * choose_num_splits (liteinfer/models/paged_kernels.py:645-693), tuned for
+ * MI355X. Returns the count (>= 1) or a negative error.
+ */
+int li_choose_num_splits(int batch, int num_kv_heads, int max_context,
+                         int num_cus, int block_kv);
+
+/*
+ * The launch plan of li_paged_decode: how many partitions the grid holds,
+ * how long each one is (0 = each sequence's context cut into num_partitions
+ * equal slices, the reference's split rule, paged_kernels.py:495-498), and
+ * how many workspace bytes the call needs. num_splits = 0 chooses (fixed
+ * length partitions, so a long context is cut more finely than a short one);
+ * num_splits >= 1 pins the reference's equal-slice split.
+ */
+int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads,
+                         int head_dim, int max_context, int num_splits,
+                         int num_cus, int block_kv, int* num_partitions,
+                         int* partition_len, size_t* workspace_bytes);
+
+/*
+ * Paged decode. Replaces paged_decode (liteinfer/models/paged_kernels.py:
+ * 696-818) and its kernels _paged_decode_kernel, _paged_decode_split_kernel
+ * and _combine_splits_kernel (:374-413, :462-629). One query per sequence:
+ *   q   [batch, num_heads, head_dim]   strides (q_stride_seq, q_stride_head, 1)
+ *   out [batch, num_heads, head_dim]   strides (out_stride_seq, out_stride_head, 1)
+ * Query head h reads KV head h / (num_heads / num_kv_heads). Row i attends
+ * to slot_table[i, 0:context_lens[i]]. fp32 accumulation; the output is
+ * rounded to `dtype` once. `workspace` must hold the bytes
+ * li_paged_decode_plan reports (it may be NULL when that is 0).
+ */
+int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+                    const void* key_pool, const void* value_pool,
+                    int64_t pool_stride_slot, int64_t pool_stride_head,
+                    const int64_t* slot_table, int64_t slot_table_stride,
+                    int max_context, const int32_t* context_lens, void* out,
+                    int64_t out_stride_seq, int64_t out_stride_head, int batch,
+                    int num_heads, int num_kv_heads, int head_dim, float scale,
+                    int num_splits, int block_kv, void* workspace,
+                    size_t workspace_bytes, int dtype, int flags, void* stream);
+
+/*
+ * Packed / chunked prefill. Replaces paged_prefill
+ * (liteinfer/models/paged_kernels.py:821-882) and _paged_prefill_kernel
+ * (:416-459). Sequence i owns query rows [query_start_loc[i],
+ * query_start_loc[i+1]) of
+ *   q   [total_queries, num_heads, head_dim]  strides (q_stride_tok, q_stride_head, 1)
+ *   out [total_queries, num_heads, head_dim]  strides (out_stride_tok, out_stride_head, 1)
+ * and those queries are the last positions of its context of
+ * context_lens[i] keys: query j of n sees keys 0 .. context_lens[i] - n + j.
+ * max_query_len sizes the grid and must be >= every sequence's query count.
+ * block_q / block_kv are the general-shape kernel's tile sizes (0 = default);
+ * the MFMA kernel uses its own.
+ */
+int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                     const void* key_pool, const void* value_pool,
+                     int64_t pool_stride_slot, int64_t pool_stride_head,
+                     const int64_t* slot_table, int64_t slot_table_stride,
+                     const int32_t* context_lens, const int32_t* query_start_loc,
+                     int batch, int max_query_len, void* out,
+                     int64_t out_stride_tok, int64_t out_stride_head,
+                     int num_heads, int num_kv_heads, int head_dim, float scale,
+                     int block_q, int block_kv, int dtype, int flags,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LITEINFER_AMD_H */

@@ -1,0 +1,95 @@
+"""Builds the HIP shared library in-tree: ``liteinfer_amd/_lib/libliteinfer_amd.so``.
+
+Every ``csrc/*.hip`` file is compiled for gfx950 by ``hipcc`` and linked into
+one shared library with a plain C ABI (``include/liteinfer_amd.h``). The
+library is loaded with ctypes, so nothing here depends on torch's extension
+machinery; it links the HIP runtime by soname, which resolves to the copy the
+process already has loaded when torch was imported first.
+
+Run as ``python -m liteinfer_amd._build``.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+import tempfile
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+CSRC_DIR = PACKAGE_DIR / "csrc"
+LIB_DIR = PACKAGE_DIR / "_lib"
+LIB_PATH = LIB_DIR / "libliteinfer_amd.so"
+
+OFFLOAD_ARCH = "gfx950"
+
+# Packed fp32 instructions stay off: some of their forms have given wrong
+# results on these machines with no error raised.
+DEVICE_FLAGS = [
+    f"--offload-arch={OFFLOAD_ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    path = Path(rocm) / "bin" / "hipcc"
+    if path.exists():
+        return str(path)
+    found = shutil.which("hipcc")
+    if found is None:
+        raise RuntimeError("hipcc not found: set ROCM_PATH or put hipcc on PATH")
+    return found
+
+
+def sources() -> list[Path]:
+    return sorted(CSRC_DIR.glob("*.hip"))
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so; that
+    # warning is harmless and is the only output dropped.
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link the library. Always rebuilds."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    with tempfile.TemporaryDirectory(prefix="liteinfer_amd_build_") as tmp:
+        objs = []
+        jobs = []
+        with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as pool:
+            for src in sources():
+                obj = Path(tmp) / (src.stem + ".o")
+                objs.append(obj)
+                jobs.append(pool.submit(_compile, src, obj))
+            for job in jobs:
+                job.result()
+        out_tmp = LIB_DIR / (LIB_PATH.name + ".tmp")
+        cmd = [hipcc(), f"--offload-arch={OFFLOAD_ARCH}", "-shared", "-fPIC", "-o", str(out_tmp), *map(str, objs)]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"link failed:\n{proc.stderr}")
+        os.replace(out_tmp, LIB_PATH)
+    if verbose:
+        print(f"built {LIB_PATH}")
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    build(verbose=True)

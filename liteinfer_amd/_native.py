@@ -1,0 +1,133 @@
+"""ctypes binding of the HIP library's C ABI (``include/liteinfer_amd.h``).
+
+The library is loaded on first use, after torch — so the HIP runtime it links
+by soname is the one torch already loaded, and a torch stream handle is a
+valid ``hipStream_t`` for it. There is no fallback: if the library is missing
+the paged path refuses to run and says how to build it.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libliteinfer_amd.so"
+
+LI_F32, LI_F16, LI_BF16 = 0, 1, 2
+LI_OK, LI_EINVAL, LI_EUNSUPPORTED, LI_ELAUNCH, LI_EWORKSPACE = 0, -1, -2, -3, -4
+LI_FLAG_FORCE_GENERIC = 1
+
+DTYPE_CODES = {torch.float32: LI_F32, torch.float16: LI_F16, torch.bfloat16: LI_BF16}
+
+# Every symbol the header declares, in declaration order.
+EXPORTED_SYMBOLS = (
+    "li_last_error_string",
+    "li_abi_version",
+    "li_kv_scatter",
+    "li_choose_num_splits",
+    "li_paged_decode_plan",
+    "li_paged_decode",
+    "li_paged_prefill",
+)
+
+_i64, _i32, _p, _f32, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+_SIGNATURES = {
+    "li_last_error_string": (ctypes.c_char_p, []),
+    "li_abi_version": (_i32, []),
+    "li_kv_scatter": (
+        _i32,
+        [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p],
+    ),
+    "li_choose_num_splits": (_i32, [_i32, _i32, _i32, _i32, _i32]),
+    "li_paged_decode_plan": (
+        _i32,
+        [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+         ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_sz)],
+    ),
+    "li_paged_decode": (
+        _i32,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
+         _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _p],
+    ),
+    "li_paged_prefill": (
+        _i32,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _p, _i32, _i32, _p, _i64, _i64,
+         _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _p],
+    ),
+}
+
+ABI_VERSION = 1
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class NativeLibraryMissing(RuntimeError):
+    """The HIP library has not been built."""
+
+
+def library_path() -> Path:
+    return LIB_PATH
+
+
+def is_built() -> bool:
+    return LIB_PATH.exists()
+
+
+def load() -> ctypes.CDLL:
+    """The loaded library, with every entry point's signature declared."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NativeLibraryMissing(
+                    f"the liteinfer_amd HIP library is not built ({LIB_PATH} is missing); "
+                    "run `python -m liteinfer_amd._build`"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (restype, argtypes) in _SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            version = lib.li_abi_version()
+            if version != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has ABI {version}, this package expects {ABI_VERSION}; rebuild it")
+            _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().li_last_error_string().decode(errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    """Raise the error a failed call reports: ValueError for bad arguments, RuntimeError otherwise."""
+    if status == LI_OK:
+        return
+    message = f"{what}: {last_error()}"
+    if status in (LI_EINVAL, LI_EUNSUPPORTED, LI_EWORKSPACE):
+        raise ValueError(message)
+    raise RuntimeError(message)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise ValueError(f"the paged kernels take float32, float16 or bfloat16, not {dtype}") from None
+
+
+def stream_handle(device: torch.device) -> int:
+    """The current torch stream of `device`, as the hipStream_t the library takes."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def i64_array(values) -> ctypes.Array:
+    return (ctypes.c_int64 * len(values))(*values)

@@ -1,0 +1,172 @@
+"""Per-sequence paged KV cache and the payloads a forward pass is handed.
+
+The protocol is liteinfer's (liteinfer/cache/kv_cache.py): a pass first
+`reserve`s room for what each sequence will hold, then gets a payload whose
+``update(k, v, layer_idx)`` stores this pass's K/V and returns a `PagedKV` —
+the layer's pool plus every address attention needs. Every address is built
+when the payload is made, so the forward holds no host work and a decode
+step can be captured.
+
+On a ROCm device the store is the HIP slot-write kernel (`kv_scatter`); the
+CPU path is torch's indexed assignment, which is what the HIP kernel is
+checked against bit for bit.
+"""
+
+from __future__ import annotations
+
+from typing import Protocol
+
+import torch
+
+from liteinfer_amd.attention import PagedKV
+from liteinfer_amd.cache.block_pool import (
+    BlockPool,
+    BlockPoolExhaustedError,
+    PackedAddresses,
+    newest_slots,
+    packed_addresses,
+    slot_table,
+)
+
+
+class KVPayload(Protocol):
+    """What one forward pass is handed in place of a KV cache (kv_cache.py:50-59)."""
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> PagedKV: ...
+
+
+def tokens_first(states: torch.Tensor) -> torch.Tensor:
+    """``[B, H, T, D]`` -> ``[B * T, H, D]`` batch-major, the order slots are in (kv_cache.py:250-253)."""
+    batch, heads, tokens, dim = states.shape
+    return states.transpose(1, 2).reshape(batch * tokens, heads, dim)
+
+
+def scatter_into(key_pool: torch.Tensor, value_pool: torch.Tensor, slots: torch.Tensor,
+                 k: torch.Tensor, v: torch.Tensor) -> None:
+    """Store ``[B, H, T, D]`` K/V rows at `slots` (B*T entries, batch-major) of one layer's pools."""
+    if key_pool.device.type == "cuda":
+        from liteinfer_amd.paged_kernels import kv_scatter
+
+        kv_scatter(key_pool, value_pool, slots, k, v)
+        return
+    flat = slots.reshape(-1)
+    key_pool[flat] = tokens_first(k)
+    value_pool[flat] = tokens_first(v)
+
+
+class KVCache:
+    """Block tables per request over one `BlockPool` (kv_cache.py:129-247)."""
+
+    def __init__(self, pool: BlockPool) -> None:
+        self._pool = pool
+        self._block_tables: dict[str, list[int]] = {}
+
+    @property
+    def pool(self) -> BlockPool:
+        return self._pool
+
+    def release(self, request_id: str) -> None:
+        """Return every block of a finished sequence to the pool."""
+        for block in self._block_tables.pop(request_id, []):
+            self._pool.free(block)
+
+    def reserve(self, request_ids: list[str], totals: list[int]) -> None:
+        """Give each sequence blocks for `totals[i]` tokens; all or nothing (kv_cache.py:145-169)."""
+        bs = self._pool.block_size
+        wanted = list(zip(request_ids, totals, strict=True))
+        short = sum(self._blocks_short_of(rid, total) for rid, total in wanted)
+        if short > self._pool.num_free_blocks:
+            raise BlockPoolExhaustedError(
+                f"KV block pool exhausted: this step needs {short} more blocks and "
+                f"{self._pool.num_free_blocks} of {self._pool.num_blocks} are free. "
+                "Increase num_gpu_blocks or reduce max_num_seqs / max_model_len."
+            )
+        for rid, total in wanted:
+            table = self._block_tables.setdefault(rid, [])
+            while len(table) * bs < total:
+                table.append(self._pool.allocate())
+
+    def _blocks_short_of(self, request_id: str, total: int) -> int:
+        held = len(self._block_tables.get(request_id, ()))
+        return max(0, -(-total // self._pool.block_size) - held)
+
+    def block_table(self, request_id: str) -> list[int]:
+        return self._block_tables[request_id]
+
+    def make_packed_payload(self, request_ids: list[str], starts: list[int], counts: list[int]) -> _PackedPayload:
+        """Payload for each sequence's `counts[i]` tokens from `starts[i]`, laid end to end."""
+        addresses = packed_addresses(self._tables(request_ids), starts, counts, self._pool.block_size, self._pool.device)
+        totals = tuple(s + c for s, c in zip(starts, counts, strict=True))
+        return _PackedPayload(self, addresses, totals, tuple(counts))
+
+    def make_decode_payload(
+        self,
+        write_slots: torch.Tensor,
+        slots: torch.Tensor,
+        context_lens: torch.Tensor,
+        num_splits: int | None = None,
+    ) -> _DecodePayload:
+        """Payload for one decode pass writing `write_slots` and reading `slots`."""
+        return _DecodePayload(self, write_slots, slots, context_lens, num_splits)
+
+    def newest_slots_for(self, request_ids: list[str], positions: list[int]) -> torch.Tensor:
+        """``[1, B]`` slot of each sequence's token at `positions[i]` — where a decode step writes."""
+        return newest_slots(self._tables(request_ids), positions, self._pool.block_size, self._pool.device)
+
+    def slot_table_for(self, request_ids: list[str], totals: list[int]) -> torch.Tensor:
+        """Each sequence's first `totals[i]` positions as slots, left-aligned."""
+        return slot_table(self._tables(request_ids), totals, self._pool.block_size, self._pool.device)
+
+    def _tables(self, request_ids: list[str]) -> list[list[int]]:
+        return [self._block_tables[rid] for rid in request_ids]
+
+    def layer_storage(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
+        return self._pool.slots(layer_idx)
+
+    def scatter(self, layer_idx: int, slots: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Store one K/V column per slot, in the order the pass holds its tokens (kv_cache.py:236-247)."""
+        keys, values = self._pool.slots(layer_idx)
+        scatter_into(keys, values, slots, k, v)
+
+
+class _PackedPayload:
+    """A pass packed end to end: whole prompts, chunks and sampled tokens (kv_cache.py:256-293)."""
+
+    def __init__(self, cache: KVCache, addresses: PackedAddresses,
+                 host_context_lens: tuple[int, ...], host_query_lens: tuple[int, ...]) -> None:
+        self._cache = cache
+        self.addresses = addresses
+        self._host_context_lens = host_context_lens
+        self._host_query_lens = host_query_lens
+        self._max_query_len = max(host_query_lens)
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> PagedKV:
+        self._cache.scatter(layer_idx, self.addresses.slots, key_states, value_states)
+        key_pool, value_pool = self._cache.layer_storage(layer_idx)
+        return PagedKV(
+            key_pool,
+            value_pool,
+            self.addresses.slot_table,
+            self.addresses.context_lens,
+            query_start_loc=self.addresses.query_start_loc,
+            max_query_len=self._max_query_len,
+            host_context_lens=self._host_context_lens,
+            host_query_lens=self._host_query_lens,
+        )
+
+
+class _DecodePayload:
+    """A decode pass: store each sequence's new token, then point at the pool (kv_cache.py:296-321)."""
+
+    def __init__(self, cache: KVCache, write_slots: torch.Tensor, slots: torch.Tensor,
+                 context_lens: torch.Tensor, num_splits: int | None) -> None:
+        self._cache = cache
+        self._write_slots = write_slots
+        self._slots = slots
+        self._context_lens = context_lens
+        self._num_splits = num_splits
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> PagedKV:
+        self._cache.scatter(layer_idx, self._write_slots, key_states, value_states)
+        key_pool, value_pool = self._cache.layer_storage(layer_idx)
+        return PagedKV(key_pool, value_pool, self._slots, self._context_lens, self._num_splits)

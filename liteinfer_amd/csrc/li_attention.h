@@ -1,0 +1,59 @@
+// Arguments and launchers shared by the attention kernels.
+#pragma once
+
+#include "li_common.h"
+
+namespace li {
+
+// One launch of an attention kernel, decode or prefill.
+//
+// Rows: a decode step has one query per sequence, query row i = sequence i
+// (qsl == nullptr); a packed pass gives sequence i the query rows
+// [qsl[i], qsl[i+1]). Either way a sequence's queries are the last positions
+// of its context of ctx[i] keys.
+//
+// Partitions (decode only): the key axis of each sequence is cut into
+// partitions of part_len keys (part_len == 0: cdiv(ctx, num_parts) keys,
+// the equal-slice rule). A sequence whose context fits in one partition is
+// written straight to `out`; otherwise every partition writes its normalised
+// fp32 output to part_o and its log2-domain log-sum-exp to part_lse, and the
+// combine kernel folds them.
+struct AttnArgs {
+  const void* q;
+  int64_t q_s0, q_s1;  // element strides: token (or sequence), head
+  const void* kp;
+  const void* vp;
+  int64_t p_s0, p_s1;  // pool strides: slot, head
+  const int64_t* st;   // slot table [batch, st_s]
+  int64_t st_s;
+  const int32_t* ctx;  // [batch]
+  const int32_t* qsl;  // [batch + 1] or nullptr for decode
+  void* out;
+  int64_t o_s0, o_s1;
+  float* part_o;    // [batch, num_heads, num_parts, head_dim] or nullptr
+  float* part_lse;  // [batch, num_heads, num_parts]
+  int batch, num_heads, num_kv_heads, groups, head_dim;
+  float scale;
+  int num_parts, part_len;
+  int block_q, block_kv;  // general-shape kernel tiles
+  int num_qblocks;        // query blocks per sequence in the grid
+  int max_query_len;      // most queries any sequence brings (prefill)
+};
+
+// Largest head_dim the general-shape kernel serves.
+constexpr int kGenericMaxHeadDim = 512;
+
+int launch_attend_generic(const AttnArgs& a, int dtype, hipStream_t s);
+int launch_combine(const AttnArgs& a, int dtype, hipStream_t s);
+
+// MFMA decode: bf16 / fp16, head_dim 64 or 128, up to 16 query heads per KV
+// head, every row 16-byte aligned. Returns LI_EUNSUPPORTED when not
+// applicable (nothing launched).
+bool decode_mfma_applies(const AttnArgs& a, int dtype);
+int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s);
+
+// MFMA prefill: same applicability rules as decode.
+bool prefill_mfma_applies(const AttnArgs& a, int dtype);
+int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t s);
+
+}  // namespace li

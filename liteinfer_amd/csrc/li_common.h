@@ -1,0 +1,90 @@
+// Shared helpers of the liteinfer_amd HIP sources: error state, element
+// types, and the small vector types the MFMA kernels move 16 bytes at a time.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdio>
+#include <cstdarg>
+
+#include "../../include/liteinfer_amd.h"
+
+namespace li {
+
+// Records `fmt` as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...);
+void clear_error();
+
+// Checks the launch that was just enqueued.
+int check_launch(const char* what);
+
+// Compute units of the current device, cached per device.
+int device_cu_count();
+
+inline int cdiv(int a, int b) { return (a + b - 1) / b; }
+inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline int dtype_size(int dtype) {
+  switch (dtype) {
+    case LI_F32: return 4;
+    case LI_F16: return 2;
+    case LI_BF16: return 2;
+    default: return 0;
+  }
+}
+
+inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+}  // namespace li
+
+// ---------------------------------------------------------------------------
+// Device-side types
+// ---------------------------------------------------------------------------
+
+typedef __bf16 li_bf16;
+typedef _Float16 li_f16;
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float floatx4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+// Converts one stored element to fp32.
+__device__ __forceinline__ float li_to_float(float x) { return x; }
+__device__ __forceinline__ float li_to_float(li_bf16 x) { return (float)x; }
+__device__ __forceinline__ float li_to_float(li_f16 x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T li_from_float(float x);
+template <>
+__device__ __forceinline__ float li_from_float<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ li_bf16 li_from_float<li_bf16>(float x) { return (li_bf16)x; }
+template <>
+__device__ __forceinline__ li_f16 li_from_float<li_f16>(float x) { return (li_f16)x; }
+
+// Bit pattern of two 16-bit elements packed low-first, from fp32 values
+// rounded to nearest even.
+template <typename T>
+__device__ __forceinline__ uint32_t li_pack2(float lo, float hi) {
+  T a = li_from_float<T>(lo), b = li_from_float<T>(hi);
+  uint16_t ua = __builtin_bit_cast(uint16_t, a);
+  uint16_t ub = __builtin_bit_cast(uint16_t, b);
+  return (uint32_t)ua | ((uint32_t)ub << 16);
+}
+
+// Wave64 reductions. Every lane gets the result.
+__device__ __forceinline__ float li_wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+__device__ __forceinline__ float li_wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}

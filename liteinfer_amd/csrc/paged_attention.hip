@@ -1,0 +1,229 @@
+// C ABI of paged decode and packed prefill: argument checks, the decode
+// partition policy, and dispatch to the MFMA or the general-shape kernels.
+#include "li_attention.h"
+
+#include <cstdlib>
+
+namespace li {
+namespace {
+
+// Decode partition policy (counterpart of choose_num_splits,
+// liteinfer/models/paged_kernels.py:645-693, re-tuned for MI355X).
+//
+// A partition is one wave64 reading its keys' K and V rows straight from the
+// pool. Only the batch rows times KV heads are free parallelism; MI355X has
+// 256 CUs, and streaming HBM at full rate wants several waves per CU in
+// flight, so each sequence's keys are cut into partitions until the grid
+// reaches kTargetWavesPerCu waves per CU. Partitions have a FIXED length
+// (the same for every row of the batch), never longer than kMaxPartition keys,
+// so a long context is cut more finely than a short one and every wave
+// carries about the same bytes whatever the spread of context lengths.
+constexpr int kTargetWavesPerCu = 8;
+constexpr int kMaxPartition = 512;
+constexpr int kMinTilesToSplit = 4;
+constexpr int kMaxPartitions = 1024;
+constexpr int kDefaultBlockKv = 64;
+
+int env_int(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return fallback;
+  const int x = std::atoi(v);
+  return x > 0 ? x : fallback;
+}
+
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// Returns the partition count of the grid and the fixed partition length
+// (0 when the whole context is one partition).
+void decode_policy(int batch, int num_kv_heads, int max_context, int num_cus, int block_kv,
+                   int* parts, int* plen) {
+  static const int target = env_int("LI_DECODE_WAVES_PER_CU", kTargetWavesPerCu);
+  static const int max_part = env_int("LI_DECODE_MAX_PARTITION", kMaxPartition);
+  const int tile = block_kv > 0 ? block_kv : kDefaultBlockKv;
+  *parts = 1;
+  *plen = 0;
+  if (max_context <= 0 || cdiv(max_context, tile) < kMinTilesToSplit) return;
+  const int64_t rows = (int64_t)std::max(batch, 1) * std::max(num_kv_heads, 1);
+  const int64_t want = std::max<int64_t>(1, (int64_t)target * num_cus / rows);
+  if (want <= 1) return;  // the unsplit grid already fills the device
+  int len = round_up((int)cdiv64(max_context, want), tile);
+  len = std::max(tile, std::min(len, std::max(tile, round_up(max_part, tile))));
+  int n = cdiv(max_context, len);
+  if (n > kMaxPartitions) {
+    len = round_up(cdiv(max_context, kMaxPartitions), tile);
+    n = cdiv(max_context, len);
+  }
+  if (n <= 1) return;
+  *parts = n;
+  *plen = len;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+size_t decode_workspace(int batch, int num_heads, int head_dim, int parts) {
+  if (parts <= 1) return 0;
+  const size_t rows = (size_t)batch * num_heads * parts;
+  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+}
+
+int check_common(int dtype, int num_heads, int num_kv_heads, int head_dim, const char* who) {
+  if (dtype_size(dtype) == 0) return fail(LI_EINVAL, "%s: unknown dtype %d", who, dtype);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(LI_EINVAL, "%s: %d query heads cannot be grouped over %d KV heads", who, num_heads, num_kv_heads);
+  if (head_dim <= 0 || head_dim > kGenericMaxHeadDim)
+    return fail(LI_EUNSUPPORTED, "%s: head_dim %d is outside 1..%d", who, head_dim, kGenericMaxHeadDim);
+  return LI_OK;
+}
+
+}  // namespace
+}  // namespace li
+
+using namespace li;
+
+extern "C" int li_choose_num_splits(int batch, int num_kv_heads, int max_context, int num_cus, int block_kv) {
+  clear_error();
+  if (batch < 0 || num_kv_heads <= 0 || max_context < 0)
+    return fail(LI_EINVAL, "li_choose_num_splits: bad extents (batch=%d kv_heads=%d max_context=%d)", batch,
+                num_kv_heads, max_context);
+  if (num_cus <= 0) num_cus = device_cu_count();
+  int parts, plen;
+  decode_policy(batch, num_kv_heads, max_context, num_cus, block_kv, &parts, &plen);
+  return parts;
+}
+
+extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,
+                                    int num_splits, int num_cus, int block_kv, int* num_partitions,
+                                    int* partition_len, size_t* workspace_bytes) {
+  clear_error();
+  if (int rc = check_common(LI_BF16, num_heads, num_kv_heads, head_dim, "li_paged_decode_plan")) return rc;
+  if (num_splits < 0) return fail(LI_EINVAL, "num_splits must be >= 1, got %d", num_splits);
+  if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_decode_plan: negative extent");
+  int parts = 1, plen = 0;
+  if (num_splits == 0) {
+    if (num_cus <= 0) num_cus = device_cu_count();
+    decode_policy(batch, num_kv_heads, max_context, num_cus, block_kv, &parts, &plen);
+  } else {
+    parts = num_splits;
+    plen = 0;
+  }
+  if (num_partitions) *num_partitions = parts;
+  if (partition_len) *partition_len = plen;
+  if (workspace_bytes) *workspace_bytes = decode_workspace(batch, num_heads, head_dim, parts);
+  return LI_OK;
+}
+
+extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* key_pool,
+                               const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                               const int64_t* slot_table, int64_t slot_table_stride, int max_context,
+                               const int32_t* context_lens, void* out, int64_t out_stride_seq,
+                               int64_t out_stride_head, int batch, int num_heads, int num_kv_heads, int head_dim,
+                               float scale, int num_splits, int block_kv, void* workspace, size_t workspace_bytes,
+                               int dtype, int flags, void* stream) {
+  clear_error();
+  if (int rc = check_common(dtype, num_heads, num_kv_heads, head_dim, "li_paged_decode")) return rc;
+  if (num_splits < 0) return fail(LI_EINVAL, "num_splits must be >= 1, got %d", num_splits);
+  if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_decode: negative extent");
+  if (batch == 0) return LI_OK;
+  if (!q || !key_pool || !value_pool || !slot_table || !context_lens || !out)
+    return fail(LI_EINVAL, "li_paged_decode: null pointer");
+
+  int parts = 1, plen = 0;
+  size_t need = 0;
+  if (int rc = li_paged_decode_plan(batch, num_heads, num_kv_heads, head_dim, max_context, num_splits, 0, block_kv,
+                                    &parts, &plen, &need))
+    return rc;
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(LI_EWORKSPACE, "li_paged_decode: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+
+  AttnArgs a{};
+  a.q = q;
+  a.q_s0 = q_stride_seq;
+  a.q_s1 = q_stride_head;
+  a.kp = key_pool;
+  a.vp = value_pool;
+  a.p_s0 = pool_stride_slot;
+  a.p_s1 = pool_stride_head;
+  a.st = slot_table;
+  a.st_s = slot_table_stride;
+  a.ctx = context_lens;
+  a.qsl = nullptr;
+  a.out = out;
+  a.o_s0 = out_stride_seq;
+  a.o_s1 = out_stride_head;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.groups = num_heads / num_kv_heads;
+  a.head_dim = head_dim;
+  a.scale = scale;
+  a.num_parts = parts;
+  a.part_len = plen;
+  a.block_q = 1;
+  a.block_kv = block_kv > 0 ? block_kv : kDefaultBlockKv;
+  a.num_qblocks = 1;
+  if (parts > 1) {
+    const size_t rows = (size_t)batch * num_heads * parts;
+    a.part_o = static_cast<float*>(workspace);
+    a.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * head_dim * sizeof(float)));
+  }
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc;
+  if (!(flags & LI_FLAG_FORCE_GENERIC) && decode_mfma_applies(a, dtype)) {
+    rc = launch_decode_mfma(a, dtype, s);
+  } else {
+    rc = launch_attend_generic(a, dtype, s);
+  }
+  if (rc) return rc;
+  if (parts > 1) rc = launch_combine(a, dtype, s);
+  return rc;
+}
+
+extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool,
+                                const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                                const int64_t* slot_table, int64_t slot_table_stride,
+                                const int32_t* context_lens, const int32_t* query_start_loc, int batch,
+                                int max_query_len, void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                                int num_heads, int num_kv_heads, int head_dim, float scale, int block_q,
+                                int block_kv, int dtype, int flags, void* stream) {
+  clear_error();
+  if (int rc = check_common(dtype, num_heads, num_kv_heads, head_dim, "li_paged_prefill")) return rc;
+  if (batch < 0 || max_query_len < 0) return fail(LI_EINVAL, "li_paged_prefill: negative extent");
+  if (batch == 0 || max_query_len == 0) return LI_OK;
+  if (!q || !key_pool || !value_pool || !slot_table || !context_lens || !query_start_loc || !out)
+    return fail(LI_EINVAL, "li_paged_prefill: null pointer");
+
+  AttnArgs a{};
+  a.q = q;
+  a.q_s0 = q_stride_tok;
+  a.q_s1 = q_stride_head;
+  a.kp = key_pool;
+  a.vp = value_pool;
+  a.p_s0 = pool_stride_slot;
+  a.p_s1 = pool_stride_head;
+  a.st = slot_table;
+  a.st_s = slot_table_stride;
+  a.ctx = context_lens;
+  a.qsl = query_start_loc;
+  a.out = out;
+  a.o_s0 = out_stride_tok;
+  a.o_s1 = out_stride_head;
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.groups = num_heads / num_kv_heads;
+  a.head_dim = head_dim;
+  a.scale = scale;
+  a.num_parts = 1;
+  a.part_len = 0;
+  a.block_kv = block_kv > 0 ? block_kv : kDefaultBlockKv;
+  a.max_query_len = max_query_len;
+
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!(flags & LI_FLAG_FORCE_GENERIC) && prefill_mfma_applies(a, dtype)) {
+    return launch_prefill_mfma(a, dtype, s);
+  }
+  a.block_q = block_q > 0 ? block_q : 16;
+  a.num_qblocks = cdiv(max_query_len, a.block_q);
+  return launch_attend_generic(a, dtype, s);
+}

@@ -1,0 +1,320 @@
+"""Attention that reads the KV pool where it lies, in hand-written HIP for MI355X.
+
+Host side of the three device kernels of liteinfer's `paged` path. The entry
+points keep the reference's names, arguments, defaults and error messages
+(liteinfer/models/paged_kernels.py:645-882), so the attention boundary and
+its tests read the same; underneath, each call is one or two launches of the
+C-ABI library in ``csrc/`` on torch's current stream:
+
+* `kv_scatter` — the KV slot-write, a bit-exact copy of this pass's K/V rows
+  into their pool slots (liteinfer/cache/kv_cache.py:236-253).
+* `paged_decode` — one query per sequence. The key axis is cut into
+  partitions (`choose_num_splits`); a sequence longer than one partition
+  writes fp32 partials and a log-sum-exp per partition, and a second launch
+  weighs them together.
+* `paged_prefill` — packed queries, causal within each sequence's chunk,
+  over the prefix the pool already holds.
+
+bf16/fp16 pools with head_dim 64 or 128 and up to 16 query heads per KV head
+run on the MFMA kernels; every other shape (fp32 above all) on a
+general-shape kernel with fp32 arithmetic. Nothing here has a CPU fallback:
+without the HIP library, or off a ROCm device, the calls raise.
+"""
+
+from __future__ import annotations
+
+import functools
+
+import torch
+
+from liteinfer_amd import _native
+
+# Keys per tile of the general-shape kernel, and the granularity of decode
+# partitions. The MFMA kernels fold 32 keys per step whatever this is.
+_BLOCK_KV = 64
+
+# Query tokens per program of the general-shape prefill kernel, and its key
+# tile (the reference's defaults, paged_kernels.py:113-114).
+_PREFILL_BLOCK_Q = 16
+_PREFILL_BLOCK_KV = 32
+
+# Partitions one sequence's decode key loop may be cut into. The reference
+# caps this at 32 (paged_kernels.py:129) because its combine holds every
+# split in registers; here the combine streams them, and a 128k-token context
+# wants far more than 32 partitions to fill 256 CUs.
+_MAX_SPLITS = 1024
+
+# Compute units assumed when no device is visible (MI355X: 8 XCDs x 32 CUs).
+_MI355X_COMPUTE_UNITS = 256
+
+_KERNELS = ("auto", "generic")
+
+
+def _flags(kernel: str) -> int:
+    if kernel not in _KERNELS:
+        raise ValueError(f"kernel must be one of {_KERNELS}, got {kernel!r}")
+    return _native.LI_FLAG_FORCE_GENERIC if kernel == "generic" else 0
+
+
+@functools.cache
+def _compute_unit_count(device_index: int) -> int:
+    """Compute units of this device. Cached: the choice below is made per layer per step."""
+    if torch.cuda.is_available():
+        return torch.cuda.get_device_properties(device_index).multi_processor_count
+    return _MI355X_COMPUTE_UNITS
+
+
+def choose_num_splits(
+    batch: int,
+    num_kv_heads: int,
+    max_context: int,
+    device_index: int,
+    block_kv: int = _BLOCK_KV,
+    num_cus: int | None = None,
+) -> int:
+    """How many partitions each sequence's decode key loop is cut into.
+
+    The counterpart of the reference's chooser (paged_kernels.py:645-693) for
+    MI355X, computed by the library (`li_choose_num_splits`) so the Python and
+    C callers agree. The unsplit grid is one wave per (sequence, KV head);
+    when that cannot keep 256 CUs streaming, each sequence's keys are cut
+    into fixed-length partitions — at most 512 keys each, at least one
+    `block_kv` tile — until the grid holds about eight waves per CU. A context
+    under four tiles is never cut, and a grid that is already full is not
+    either. The answer is a function of host integers only (`max_context` is
+    the slot table's width), so a captured graph keeps the count it recorded.
+    """
+    if num_cus is None:
+        num_cus = _compute_unit_count(device_index)
+    splits = _native.load().li_choose_num_splits(batch, num_kv_heads, max_context, num_cus, block_kv)
+    if splits < 1:
+        _native.check(splits, "choose_num_splits")
+    return splits
+
+
+def _require_device_tensors(*tensors: torch.Tensor) -> torch.device:
+    device = tensors[0].device
+    if device.type != "cuda" or torch.version.hip is None:
+        raise RuntimeError(f"the paged kernels are HIP kernels and need a ROCm device, got {device}")
+    for t in tensors:
+        if t.device != device:
+            raise ValueError(f"all operands must be on {device}, one is on {t.device}")
+    return device
+
+
+def _check_pools(key_pool: torch.Tensor, value_pool: torch.Tensor) -> None:
+    if key_pool.stride() != value_pool.stride():
+        raise ValueError("key and value pools must be laid out identically")
+    if key_pool.dim() != 3 or key_pool.shape != value_pool.shape:
+        raise ValueError(f"pools must be [num_slots, kv_heads, head_dim], got {tuple(key_pool.shape)}")
+    if key_pool.stride(2) != 1:
+        raise ValueError("the pools' head_dim axis must be contiguous")
+    if key_pool.dtype != value_pool.dtype:
+        raise ValueError("key and value pools must share a dtype")
+
+
+def _as_index(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    return t if t.dtype == dtype else t.to(dtype)
+
+
+def _last_dim_contiguous(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def kv_scatter(
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    slots: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+) -> None:
+    """Store one K/V column per slot, in the order the pass holds its tokens.
+
+    `k` and `v` are ``[B, H, T, D]`` (any strides); `slots` holds ``B * T``
+    entries taken batch-major, ``[1, T]`` for a packed pass or ``[1, B]`` for a
+    decode step (kv_cache.py:236-247). The pools are this layer's
+    ``[num_slots, H, D]`` stores and are written in place, bit for bit.
+    """
+    device = _require_device_tensors(key_pool, value_pool, slots, k, v)
+    _check_pools(key_pool, value_pool)
+    if k.dim() != 4 or k.shape != v.shape:
+        raise ValueError(f"k and v must both be [batch, heads, tokens, head_dim], got {tuple(k.shape)}, {tuple(v.shape)}")
+    batch, heads, tokens, head_dim = k.shape
+    if heads != key_pool.shape[1] or head_dim != key_pool.shape[2]:
+        raise ValueError(f"k rows {heads}x{head_dim} do not match the pool's {tuple(key_pool.shape[1:])}")
+    if k.dtype != key_pool.dtype or v.dtype != key_pool.dtype:
+        raise ValueError(f"k/v dtype {k.dtype} does not match the pool's {key_pool.dtype}")
+    flat_slots = _as_index(slots.reshape(-1), torch.int64).contiguous()
+    if flat_slots.numel() != batch * tokens:
+        raise ValueError(f"{flat_slots.numel()} slots for {batch * tokens} tokens")
+    lib = _native.load()
+    status = lib.li_kv_scatter(
+        k.data_ptr(), v.data_ptr(),
+        _native.i64_array(k.stride()), _native.i64_array(v.stride()),
+        batch, tokens, flat_slots.data_ptr(),
+        key_pool.data_ptr(), value_pool.data_ptr(),
+        key_pool.shape[0], key_pool.stride(0), key_pool.stride(1),
+        heads, head_dim, _native.dtype_code(key_pool.dtype),
+        _native.stream_handle(device),
+    )
+    _native.check(status, "kv_scatter")
+
+
+def paged_decode(
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    slot_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    scaling: float,
+    num_kv_groups: int,
+    block_kv: int = _BLOCK_KV,
+    num_splits: int | None = None,
+    *,
+    kernel: str = "auto",
+) -> torch.Tensor:
+    """Attend one query per sequence over the KV each sequence's slots address.
+
+    Args:
+        query: ``[batch, num_heads, head_dim]`` — the decode token's queries.
+        key_pool: this layer's flat key store, ``[num_slots, num_kv_heads, head_dim]``.
+        value_pool: the matching value store.
+        slot_table: ``[batch, max_context]`` physical slot per logical position,
+            left-aligned; columns past a row's context are never read.
+        context_lens: ``[batch]`` real cached tokens per sequence.
+        scaling: softmax scale, normally ``head_dim ** -0.5``.
+        num_kv_groups: query heads per KV head.
+        block_kv: key tile of the general-shape kernel and the granularity of
+            the chosen partitions.
+        num_splits: ``None`` lets `choose_num_splits` cut the key axis into
+            fixed-length partitions; an integer pins the reference's rule, each
+            sequence's context cut into that many equal slices.
+        kernel: ``"auto"`` (MFMA where it applies) or ``"generic"``.
+
+    Returns:
+        ``[batch, num_heads, head_dim]``, same dtype as ``query``.
+    """
+    if key_pool.stride() != value_pool.stride():
+        raise ValueError("key and value pools must be laid out identically")
+    if num_splits is not None and num_splits < 1:
+        raise ValueError(f"num_splits must be >= 1, got {num_splits}")
+    device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens)
+    _check_pools(key_pool, value_pool)
+    batch, num_heads, head_dim = query.shape
+    if query.dtype != key_pool.dtype:
+        raise ValueError(f"query dtype {query.dtype} does not match the pool's {key_pool.dtype}")
+    if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:
+        raise ValueError(
+            f"{num_heads} query heads in groups of {num_kv_groups} do not match {key_pool.shape[1]} KV heads"
+        )
+    if head_dim != key_pool.shape[2]:
+        raise ValueError(f"query head_dim {head_dim} does not match the pool's {key_pool.shape[2]}")
+    query = _last_dim_contiguous(query)
+    slot_table = _as_index(slot_table, torch.int64)
+    if slot_table.stride(-1) != 1:
+        slot_table = slot_table.contiguous()
+    context_lens = _as_index(context_lens, torch.int32).contiguous()
+    num_kv_heads = key_pool.shape[1]
+    max_context = slot_table.shape[1]
+
+    lib = _native.load()
+    parts, plen, need = _native.ctypes.c_int(), _native.ctypes.c_int(), _native.ctypes.c_size_t()
+    status = lib.li_paged_decode_plan(
+        batch, num_heads, num_kv_heads, head_dim, max_context, num_splits or 0,
+        _compute_unit_count(device.index or 0), block_kv,
+        _native.ctypes.byref(parts), _native.ctypes.byref(plen), _native.ctypes.byref(need),
+    )
+    _native.check(status, "paged_decode")
+
+    out = torch.empty_like(query)
+    workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
+    status = lib.li_paged_decode(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
+        slot_table.data_ptr(), slot_table.stride(0), max_context,
+        context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+        batch, num_heads, num_kv_heads, head_dim, float(scaling),
+        num_splits or 0, block_kv,
+        workspace.data_ptr() if workspace is not None else None, need.value,
+        _native.dtype_code(query.dtype), _flags(kernel), _native.stream_handle(device),
+    )
+    _native.check(status, "paged_decode")
+    return out
+
+
+def paged_prefill(
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    slot_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    query_start_loc: torch.Tensor,
+    max_query_len: int,
+    scaling: float,
+    num_kv_groups: int,
+    block_kv: int = _PREFILL_BLOCK_KV,
+    block_q: int = _PREFILL_BLOCK_Q,
+    *,
+    kernel: str = "auto",
+) -> torch.Tensor:
+    """Attend each sequence's chunk of queries over the KV its slots address, causally.
+
+    Sequence ``i``'s queries are rows ``[query_start_loc[i], query_start_loc[i +
+    1])`` of `query`, and they are the *last* positions of its context: the
+    chunk's own K/V are already in the pool, written by the layer's payload just
+    before this call (paged_kernels.py:821-882).
+
+    Args:
+        query: ``[total_queries, num_heads, head_dim]``, sequences end to end,
+            any strides with the last axis contiguous.
+        key_pool: this layer's flat key store, ``[num_slots, num_kv_heads, head_dim]``.
+        value_pool: the matching value store.
+        slot_table: ``[batch, max_context]`` physical slot per logical position.
+        context_lens: ``[batch]`` tokens each sequence holds, its chunk included.
+        query_start_loc: ``[batch + 1]`` int32 prefix sums of the chunk lengths.
+        max_query_len: longest chunk, which sizes the grid and so is a host int.
+        scaling: softmax scale, normally ``head_dim ** -0.5``.
+        num_kv_groups: query heads per KV head.
+        block_kv, block_q: tiles of the general-shape kernel.
+        kernel: ``"auto"`` (MFMA where it applies) or ``"generic"``.
+
+    Returns:
+        ``[total_queries, num_heads, head_dim]`` with the strides of `query`.
+    """
+    if key_pool.stride() != value_pool.stride():
+        raise ValueError("key and value pools must be laid out identically")
+    device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens, query_start_loc)
+    _check_pools(key_pool, value_pool)
+    _, num_heads, head_dim = query.shape
+    if query.dtype != key_pool.dtype:
+        raise ValueError(f"query dtype {query.dtype} does not match the pool's {key_pool.dtype}")
+    if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:
+        raise ValueError(
+            f"{num_heads} query heads in groups of {num_kv_groups} do not match {key_pool.shape[1]} KV heads"
+        )
+    if head_dim != key_pool.shape[2]:
+        raise ValueError(f"query head_dim {head_dim} does not match the pool's {key_pool.shape[2]}")
+    query = _last_dim_contiguous(query)
+    slot_table = _as_index(slot_table, torch.int64)
+    if slot_table.stride(-1) != 1:
+        slot_table = slot_table.contiguous()
+    context_lens = _as_index(context_lens, torch.int32).contiguous()
+    query_start_loc = _as_index(query_start_loc, torch.int32).contiguous()
+    batch = context_lens.shape[0]
+    if query_start_loc.shape[0] != batch + 1:
+        raise ValueError(f"query_start_loc has {query_start_loc.shape[0]} entries for {batch} sequences")
+    num_kv_heads = key_pool.shape[1]
+
+    out = torch.empty_like(query)
+    lib = _native.load()
+    status = lib.li_paged_prefill(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
+        slot_table.data_ptr(), slot_table.stride(0),
+        context_lens.data_ptr(), query_start_loc.data_ptr(), batch, int(max_query_len),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        num_heads, num_kv_heads, head_dim, float(scaling), block_q, block_kv,
+        _native.dtype_code(query.dtype), _flags(kernel), _native.stream_handle(device),
+    )
+    _native.check(status, "paged_prefill")
+    return out

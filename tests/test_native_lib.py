@@ -1,0 +1,118 @@
+"""The C-ABI library loads, exports what the header declares, and checks arguments (CPU; no kernel runs)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from liteinfer_amd import _native
+from liteinfer_amd.paged_kernels import _MAX_SPLITS, choose_num_splits
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "liteinfer_amd.h"
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"\b(li_[a-z0-9_]+)\s*\(", text)
+
+
+def test_library_is_built_and_loads():
+    assert _native.is_built(), "run `python -m liteinfer_amd._build` (or __graft_entry__.build())"
+    lib = _native.load()
+    assert lib.li_abi_version() == _native.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    assert sorted(declared) == sorted(_native.EXPORTED_SYMBOLS)
+    lib = ctypes.CDLL(str(_native.library_path()))
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def _splits(batch, kv_heads, max_context, cus=256):
+    return choose_num_splits(batch, kv_heads, max_context, device_index=0, block_kv=64, num_cus=cus)
+
+
+def test_a_batch_that_already_fills_the_device_is_not_split():
+    assert _splits(batch=256, kv_heads=8, max_context=1024) == 1
+
+
+def test_a_single_sequence_splits_its_key_loop():
+    assert _splits(batch=1, kv_heads=1, max_context=4096) > 1
+
+
+def test_the_split_count_never_exceeds_the_cap():
+    assert _splits(batch=1, kv_heads=1, max_context=1 << 20) <= _MAX_SPLITS
+
+
+def test_a_context_with_too_little_to_cut_is_not_split():
+    assert _splits(batch=1, kv_heads=1, max_context=128) == 1
+
+
+def test_no_partition_is_shorter_than_one_key_tile():
+    assert _splits(batch=1, kv_heads=1, max_context=256) == 4
+
+
+def test_a_longer_context_is_cut_more_finely():
+    assert _splits(batch=1, kv_heads=8, max_context=4096) > _splits(batch=1, kv_heads=8, max_context=256)
+
+
+def test_partitions_never_exceed_512_keys_so_waves_carry_equal_work():
+    # Llama-3-8B decode at batch 64 over contexts up to 8192: 16 partitions of 512.
+    assert _splits(batch=64, kv_heads=8, max_context=8192) == 16
+    # batch 8 over 131072: 256 partitions of 512.
+    assert _splits(batch=8, kv_heads=8, max_context=131072) == 256
+
+
+def _plan(**kw):
+    args = dict(batch=4, num_heads=32, num_kv_heads=8, head_dim=128, max_context=4096, num_splits=0, num_cus=256,
+                block_kv=64)
+    args.update(kw)
+    lib = _native.load()
+    parts, plen, need = ctypes.c_int(), ctypes.c_int(), ctypes.c_size_t()
+    status = lib.li_paged_decode_plan(*args.values(), ctypes.byref(parts), ctypes.byref(plen), ctypes.byref(need))
+    return status, parts.value, plen.value, need.value
+
+
+def test_plan_sizes_the_workspace_for_its_partitions():
+    status, parts, plen, need = _plan()
+    assert status == 0 and parts > 1 and plen % 64 == 0
+    rows = 4 * 32 * parts
+    assert need >= rows * 128 * 4 + rows * 4
+
+
+def test_plan_pins_the_reference_split_rule_when_asked():
+    status, parts, plen, _ = _plan(num_splits=5)
+    assert (status, parts, plen) == (0, 5, 0)
+    status, parts, _, need = _plan(num_splits=1)
+    assert (status, parts, need) == (0, 1, 0)
+
+
+def test_plan_rejects_bad_arguments_with_a_message():
+    status, *_ = _plan(num_heads=30)
+    assert status == _native.LI_EINVAL
+    assert "cannot be grouped" in _native.last_error()
+    status, *_ = _plan(num_splits=-1)
+    assert status == _native.LI_EINVAL
+    assert "num_splits must be >= 1" in _native.last_error()
+
+
+def test_check_raises_the_reported_message():
+    _plan(num_heads=30)
+    with pytest.raises(ValueError, match="cannot be grouped"):
+        _native.check(_native.LI_EINVAL, "plan")
+
+
+def test_scatter_rejects_null_pointers_before_launching():
+    lib = _native.load()
+    strides = _native.i64_array([0, 0, 0, 1])
+    status = lib.li_kv_scatter(None, None, strides, strides, 1, 1, None, None, None, 16, 16, 8, 2, 8,
+                               _native.LI_BF16, None)
+    assert status == _native.LI_EINVAL
+    assert "null pointer" in _native.last_error()

@@ -1,0 +1,143 @@
+"""The HIP paged decode answers what the oracle answers.
+
+Restates the reference's decode tests (tests/unit/test_paged_decode.py) with
+the fp64 oracle as the answer: fp32 within rtol = atol = 1e-5, bf16 within
+atol 2^-6, and BASELINE's bar for bf16 (max-abs 2e-2, mean-abs 2e-3). Both
+kernels are checked: the MFMA kernel (bf16/fp16, head_dim 64/128, groups up to
+16) and the general-shape kernel (everything, fp32 above all).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from liteinfer_amd.paged_kernels import paged_decode
+from tests.helpers import PagedBatch, assert_within, to_numpy
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(b: PagedBatch, **kw) -> torch.Tensor:
+    return paged_decode(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.scaling, b.groups, **kw)
+
+
+def _fp32_close(actual, expected):
+    np.testing.assert_allclose(to_numpy(actual), expected, rtol=1e-5, atol=1e-5)
+
+
+# --- the reference's cases, fp32 through the general-shape kernel ----------------------
+
+
+def test_float32_matches_the_oracle():
+    b = PagedBatch([6, 4, 1])
+    _fp32_close(_run(b), b.oracle())
+
+
+@pytest.mark.parametrize("block_kv", [16, 32, 64, 128])
+def test_the_answer_does_not_depend_on_the_key_tile(block_kv):
+    b = PagedBatch([200, 65, 64, 63, 17, 1])
+    _fp32_close(_run(b, block_kv=block_kv), b.oracle())
+
+
+def test_a_group_that_is_not_a_power_of_two():
+    b = PagedBatch([70, 5], num_heads=10, num_kv_heads=2)
+    _fp32_close(_run(b), b.oracle())
+
+
+def test_no_grouped_query_heads():
+    b = PagedBatch([9, 3], num_kv_heads=8)
+    _fp32_close(_run(b), b.oracle())
+
+
+@pytest.mark.parametrize("head_dim", [96, 80, 48, 24])
+def test_head_dims_off_the_fast_path(head_dim):
+    b = PagedBatch([70, 5], head_dim=head_dim)
+    _fp32_close(_run(b), b.oracle())
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 3, 5, 8, 32])
+def test_the_answer_does_not_depend_on_the_split_count(num_splits):
+    b = PagedBatch([200, 65, 64, 63, 17, 1])
+    _fp32_close(_run(b, num_splits=num_splits), b.oracle())
+
+
+def test_split_and_unsplit_agree():
+    b = PagedBatch([300, 129, 7])
+    torch.testing.assert_close(_run(b, num_splits=11), _run(b, num_splits=1), rtol=1e-5, atol=1e-5)
+
+
+def test_splits_past_a_short_context_contribute_nothing():
+    b = PagedBatch([200, 3])
+    _fp32_close(_run(b, num_splits=8), b.oracle())
+
+
+def test_padding_columns_are_never_read():
+    b = PagedBatch([200, 65, 3], dtype=torch.bfloat16)
+    for kernel in ("auto", "generic"):
+        first = _run(b, kernel=kernel)
+        table = b.slot_table.clone()
+        cols = torch.arange(table.shape[1], device=table.device)
+        pad = cols[None, :] >= b.context_lens_t[:, None]
+        table[pad] = torch.randint(1, 512, (int(pad.sum()),), device=table.device)
+        b2 = b
+        b2.slot_table = table
+        assert torch.equal(_run(b2, kernel=kernel), first)
+
+
+def test_pools_laid_out_differently_are_refused():
+    b = PagedBatch([4])
+    with pytest.raises(ValueError, match="laid out identically"):
+        paged_decode(b.query, b.key_pool, b.value_pool.transpose(1, 2), b.slot_table, b.context_lens_t, b.scaling,
+                     b.groups)
+
+
+def test_fewer_than_one_split_is_refused():
+    b = PagedBatch([4])
+    with pytest.raises(ValueError, match="num_splits must be >= 1"):
+        _run(b, num_splits=0)
+
+
+# --- bf16 / fp16 through both kernels --------------------------------------------------
+
+
+@pytest.mark.parametrize("kernel", ["auto", "generic"])
+@pytest.mark.parametrize("num_splits", [None, 1, 11])
+def test_bfloat16_within_rounding(kernel, num_splits):
+    b = PagedBatch([300, 129, 7], dtype=torch.bfloat16)
+    assert_within(_run(b, kernel=kernel, num_splits=num_splits), b.oracle(), 2 ** -6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (8, 8), (10, 2), (32, 4), (16, 1)])
+def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads):
+    """Every group the MFMA kernel takes (1, 4, 5, 8, 16), contexts straddling 32-key tiles."""
+    b = PagedBatch([1, 31, 32, 33, 100, 257, 1000], dtype=dtype, num_heads=num_heads, num_kv_heads=num_kv_heads,
+                   head_dim=head_dim, num_slots=4096, seed=2)
+    want = b.oracle()
+    for splits in (None, 1, 3):
+        assert_within(_run(b, num_splits=splits), want, 2 ** -6, 2e-3)
+
+
+def test_mfma_and_general_kernels_agree():
+    b = PagedBatch([513, 64, 2000, 1], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128,
+                   num_slots=8192, seed=4)
+    fast = _run(b)
+    slow = _run(b, kernel="generic")
+    assert_within(fast, to_numpy(slow).astype(np.float64), 2 ** -7)
+
+
+def test_strided_query_is_served():
+    b = PagedBatch([77, 5], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128, num_slots=1024)
+    wide = torch.zeros(b.query.shape[0], b.query.shape[1], 256, dtype=b.query.dtype, device=b.query.device)
+    wide[..., :128] = b.query
+    b.query = wide[..., :128]
+    assert_within(_run(b), b.oracle(), 2 ** -6)
+
+
+def test_long_context_is_partitioned_and_combined():
+    b = PagedBatch([20000, 3000], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128,
+                   num_slots=32768, seed=9)
+    assert_within(_run(b), b.oracle(), 2e-2, 2e-3)

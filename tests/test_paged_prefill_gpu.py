@@ -1,0 +1,97 @@
+"""The HIP packed/chunked prefill answers what the oracle answers.
+
+Restates the reference's prefill tests (tests/unit/test_paged_prefill.py)
+with the fp64 oracle as the answer, for both the general-shape kernel and the
+MFMA kernel.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from liteinfer_amd.paged_kernels import paged_decode, paged_prefill
+from tests.helpers import PagedBatch, assert_within, to_numpy
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(b: PagedBatch, **kw) -> torch.Tensor:
+    return paged_prefill(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.query_start_loc,
+                         max(b.query_lens), b.scaling, b.groups, **kw)
+
+
+def _fp32_close(actual, expected):
+    np.testing.assert_allclose(to_numpy(actual), expected, rtol=1e-5, atol=1e-5)
+
+
+def test_a_chunk_reads_its_prefix_and_its_own_past():
+    b = PagedBatch([23], [5], num_slots=2048)
+    _fp32_close(_run(b), b.oracle())
+
+
+def test_a_whole_prompt_is_the_chunk_whose_context_is_itself():
+    b = PagedBatch([37], [37], num_slots=2048)
+    _fp32_close(_run(b), b.oracle())
+
+
+def test_decode_rows_beside_chunks_in_one_launch():
+    b = PagedBatch([90, 60, 3, 7], [1, 40, 1, 7], num_slots=2048)
+    _fp32_close(_run(b), b.oracle())
+
+
+@pytest.mark.parametrize("block_q", [1, 4, 16, 32])
+def test_the_answer_does_not_depend_on_the_query_block(block_q):
+    b = PagedBatch([100, 16, 47, 9], [33, 16, 15, 1], num_slots=2048)
+    _fp32_close(_run(b, block_q=block_q), b.oracle())
+
+
+@pytest.mark.parametrize("block_kv", [16, 64, 128])
+def test_the_answer_does_not_depend_on_the_key_tile(block_kv):
+    b = PagedBatch([200, 65], [70, 3], num_slots=2048)
+    _fp32_close(_run(b, block_kv=block_kv), b.oracle())
+
+
+@pytest.mark.parametrize(
+    ("num_heads", "num_kv_heads", "head_dim"),
+    [(8, 8, 16), (8, 1, 16), (10, 2, 16), (8, 2, 80)],
+    ids=["no-grouping", "one-kv-head", "group-not-a-power-of-two", "head-dim-not-a-power-of-two"],
+)
+def test_groupings_and_head_dims(num_heads, num_kv_heads, head_dim):
+    b = PagedBatch([50, 30], [19, 1], num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                   num_slots=2048)
+    _fp32_close(_run(b), b.oracle())
+
+
+def test_one_query_per_sequence_equals_decode():
+    b = PagedBatch([90, 17, 1], [1, 1, 1], num_slots=2048)
+    decode = paged_decode(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.scaling, b.groups,
+                          num_splits=1)
+    _fp32_close(_run(b), to_numpy(decode).astype(np.float64))
+
+
+def test_strided_query_and_output_layout_are_kept():
+    """The boundary hands over `query.squeeze(0).transpose(0, 1)`, a strided view."""
+    b = PagedBatch([130, 64, 12], [33, 1, 12], dtype=torch.bfloat16, num_slots=2048)
+    heads_first = b.query.transpose(0, 1).contiguous()  # [H, T, D]
+    b.query = heads_first.transpose(0, 1)               # [T, H, D] view, token stride D
+    out = _run(b)
+    assert out.stride() == b.query.stride()
+    assert_within(out, b.oracle(), 2 ** -6)
+
+
+@pytest.mark.parametrize("kernel", ["auto", "generic"])
+def test_bfloat16_within_rounding(kernel):
+    b = PagedBatch([130, 64, 12], [33, 1, 12], dtype=torch.bfloat16, num_slots=2048)
+    assert_within(_run(b, kernel=kernel), b.oracle(), 2 ** -6)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (8, 8), (10, 2), (16, 1)])
+def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads):
+    """Chunks straddling every tile boundary, over prefixes and alone, beside decode rows."""
+    b = PagedBatch([1, 40, 300, 129, 64, 700], [1, 33, 200, 1, 64, 31], dtype=dtype, num_heads=num_heads,
+                   num_kv_heads=num_kv_heads, head_dim=head_dim, num_slots=4096, seed=6)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
