@@ -1,0 +1,280 @@
+"""Benchmark of liteinfer's `paged` attention path on one MI355X.
+
+A step is one layer's share of a decode step at BASELINE config 2
+(Llama-3-8B geometry: 32/8 heads, head_dim 128, bf16, block 16, batch 64,
+contexts uniform in [512, 8192], pool of 65,536 blocks with seeded shuffled
+block tables): the slot-write of each sequence's new K/V, then paged decode
+through the `paged` boundary. Inputs are synthetic N(0, 1) and resident in HBM
+before the clock starts.
+
+`value` is algorithmic bytes per step / step time, in GB/s: every context
+token's K and V rows for all KV heads plus its int64 slot index, the queries
+and outputs, and the slot-write's reads and writes. `roofline` rates the
+decode call (the partition kernel plus the partition combine, timed with HIP
+events on the stream they run on) against MI355X's 8 TB/s. Config 3's packed
+prefill (TFLOP/s of visible causal pairs) and config 4's long-context decode
+are reported beside it. `cpu_baseline` times the dense eager attention
+(oracle/baseline.py) in fp32 on this host's cores over a bounded sample of the
+same step.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from liteinfer_amd import _native  # noqa: E402
+from liteinfer_amd.attention import PagedKV, paged_attention  # noqa: E402
+from liteinfer_amd.cache.kv_cache import scatter_into  # noqa: E402
+from liteinfer_amd.workloads import decode_step, packed_step  # noqa: E402
+
+METRIC = "paged-decode HBM GB/s (% of peak); prefill attn TFLOP/s; e2e output tok/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_FILE = ROOT / "profiles" / "decode_c2_traffic.json"
+
+
+def decode_bytes(ctxs, geo, elem=2) -> int:
+    """K and V rows of every context token for all KV heads, its int64 slot, q in and out."""
+    tokens = sum(ctxs)
+    return tokens * (2 * geo.num_kv_heads * geo.head_dim * elem + 8) + 2 * len(ctxs) * geo.num_heads * geo.head_dim * elem
+
+
+def scatter_bytes(tokens, geo, elem=2) -> int:
+    """Read the new K and V rows, write them into the pool, read the int64 slots."""
+    return tokens * (4 * geo.num_kv_heads * geo.head_dim * elem + 8)
+
+
+def prefill_flops(qlens, ctxs, geo) -> int:
+    """4 * heads * head_dim flops per visible (query, key) pair (QK^T and PV)."""
+    pairs = sum(q * (c - q) + q * (q + 1) // 2 for q, c in zip(qlens, ctxs))
+    return 4 * geo.num_heads * geo.head_dim * pairs
+
+
+def _time_decode(step, steps, warmup):
+    geo = step.geometry
+    kv = PagedKV(step.key_pool, step.value_pool, step.slot_table, step.context_lens)
+    q = step.query.unsqueeze(2)
+
+    def one():
+        scatter_into(step.key_pool, step.value_pool, step.write_slots, step.new_k, step.new_v)
+        return paged_attention(q, kv, geo.scaling, geo.groups)
+
+    for _ in range(warmup):
+        one()
+    stream = torch.cuda.current_stream()
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for a, b in marks:
+        scatter_into(step.key_pool, step.value_pool, step.write_slots, step.new_k, step.new_v)
+        a.record(stream)
+        paged_attention(q, kv, geo.scaling, geo.groups)
+        b.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    decode_ms = [a.elapsed_time(b) for a, b in marks]
+    return wall, decode_ms
+
+
+def _time_prefill(step, steps, warmup):
+    geo = step.geometry
+    kv = PagedKV(step.key_pool, step.value_pool, step.slot_table, step.context_lens,
+                 query_start_loc=step.query_start_loc, max_query_len=step.max_query_len,
+                 host_context_lens=tuple(step.host_context_lens), host_query_lens=tuple(step.host_query_lens))
+    q = step.query.transpose(0, 1).unsqueeze(0)
+    scatter_into(step.key_pool, step.value_pool, step.write_slots, step.new_k, step.new_v)
+    for _ in range(warmup):
+        paged_attention(q, kv, geo.scaling, geo.groups)
+    stream = torch.cuda.current_stream()
+    marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for a, b in marks:
+        a.record(stream)
+        paged_attention(q, kv, geo.scaling, geo.groups)
+        b.record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in marks]
+
+
+def cpu_baseline(step, max_seconds: float = 20.0) -> dict:
+    """Dense eager attention (fp32, torch CPU threads) over the first sequences of the step."""
+    from oracle import baseline
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    geo = step.geometry
+    n = 8
+    ctxs = step.host_context_lens[:n]
+    width = max(ctxs)
+    table = step.slot_table[:n, :width]
+    uniq, inverse = torch.unique(table, return_inverse=True)
+    kp = step.key_pool[uniq].float().cpu()
+    vp = step.value_pool[uniq].float().cpu()
+    q = step.query[:n].float().cpu()
+    local = inverse.cpu()
+    ctx_t = torch.tensor(ctxs)
+    baseline.decode("eager", q, kp, vp, local, ctx_t, geo.scaling, geo.groups)  # warm-up
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 5 and time.perf_counter() - t_start < max_seconds:
+        t0 = time.perf_counter()
+        baseline.decode("eager", q, kp, vp, local, ctx_t, geo.scaling, geo.groups)
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    t0 = time.perf_counter()
+    baseline.decode("sdpa", q, kp, vp, local, ctx_t, geo.scaling, geo.groups)
+    sdpa_sec = time.perf_counter() - t0
+    nbytes = decode_bytes(ctxs, geo)
+    cpu_model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / sec / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"dense eager attention (oracle/baseline.py, fp32 torch) over the first {n} of config 2's 64 "
+                   f"sequences ({sum(ctxs)} context tokens), median of {len(times)} calls = {sec * 1e3:.1f} ms; "
+                   f"sdpa one call = {sdpa_sec * 1e3:.1f} ms ({nbytes / sdpa_sec / 1e9:.3f} GB/s); CPU: {cpu_model}"),
+    }
+
+
+def _traffic():
+    if TRAFFIC_FILE.exists():
+        try:
+            return json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-secondary", action="store_true", help="skip configs 3 and 4")
+    args = parser.parse_args()
+
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build's paged path has no multi-GPU component "
+              "(decode shards by sequence or KV head with no exchange inside attention); run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    _native.load()
+    torch.cuda.set_device(0)
+
+    step = decode_step("c2", seed=args.seed)
+    geo = step.geometry
+    wall, decode_ms = _time_decode(step, args.steps, args.warmup)
+    ms_per_step = wall / args.steps * 1e3
+    d_bytes = decode_bytes(step.host_context_lens, geo)
+    s_bytes = scatter_bytes(step.batch, geo)
+    value = (d_bytes + s_bytes) / (ms_per_step * 1e-3) / 1e9
+    decode_avg_ms = statistics.mean(decode_ms)
+    achieved = d_bytes / (decode_avg_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) q/K/V, seeded shuffled block tables",
+        "config": {
+            "workload": "c2: one layer's decode step (slot-write + paged decode), Llama-3-8B attention geometry",
+            "batch": step.batch,
+            "context_tokens": sum(step.host_context_lens),
+            "context_range": [min(step.host_context_lens), max(step.host_context_lens)],
+            "num_heads": geo.num_heads,
+            "num_kv_heads": geo.num_kv_heads,
+            "head_dim": geo.head_dim,
+            "block_size": 16,
+            "pool_blocks": 65536,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "kernel": "paged decode call (decode_mfma + combine_parts)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": _traffic(),
+            "algorithmic_bytes_per_launch": d_bytes,
+            "avg_launch_us": round(decode_avg_ms * 1e3, 2),
+        },
+    }
+
+    if not args.no_secondary:
+        secondary = {}
+        del step
+        torch.cuda.empty_cache()
+        c4 = decode_step("c4", seed=args.seed)
+        _, c4_ms = _time_decode(c4, max(10, args.steps // 4), 3)
+        c4_bytes = decode_bytes(c4.host_context_lens, c4.geometry)
+        c4_avg = statistics.mean(c4_ms)
+        secondary["decode_c4"] = {
+            "avg_us": round(c4_avg * 1e3, 2),
+            "GB/s": round(c4_bytes / (c4_avg * 1e-3) / 1e9, 1),
+            "frac_hbm": round(c4_bytes / (c4_avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "context_tokens": sum(c4.host_context_lens),
+        }
+        del c4
+        torch.cuda.empty_cache()
+        c3 = packed_step("c3", seed=args.seed)
+        c3_ms = _time_prefill(c3, max(10, args.steps // 4), 3)
+        c3_avg = statistics.mean(c3_ms)
+        flops = prefill_flops(c3.host_query_lens, c3.host_context_lens, c3.geometry)
+        secondary["prefill_c3"] = {
+            "avg_us": round(c3_avg * 1e3, 2),
+            "TFLOP/s": round(flops / (c3_avg * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flops / (c3_avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "visible_pair_flops": flops,
+            "query_tokens": sum(c3.host_query_lens),
+        }
+        result["secondary"] = secondary
+        del c3
+        torch.cuda.empty_cache()
+        step = None
+
+    if not args.no_cpu_baseline:
+        sample_step = decode_step("c2", seed=args.seed)
+        result["cpu_baseline"] = cpu_baseline(sample_step)
+
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

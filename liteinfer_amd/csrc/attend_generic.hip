@@ -140,9 +140,12 @@ __global__ __launch_bounds__(64) void attend_generic(AttnArgs a) {
 // Folds a sequence's partitions: w_p = 2^(lse_p - max lse), out = sum w_p o_p
 // / sum w_p (paged_kernels.py:574-629, in the log2 domain). One wave per
 // (head, sequence); a sequence that fit one partition was written directly.
+// Lane j holds the weights of partitions j, j + 64, ...; the partial rows are
+// read eight partitions at a time so their loads overlap.
 template <typename T>
 __global__ __launch_bounds__(64) void combine_parts(AttnArgs a) {
   constexpr int kMaxC = kGenericMaxHeadDim / 64;
+  constexpr int kBatch = 8;
   const int lane = threadIdx.x;
   const int head = blockIdx.x % a.num_heads;
   const int seq = blockIdx.x / a.num_heads;
@@ -158,18 +161,33 @@ __global__ __launch_bounds__(64) void combine_parts(AttnArgs a) {
   float mx = -INFINITY;
   for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, lse[p]);
   mx = li_wave_max(mx);
+  float wsum = 0.f;
+  for (int p = lane; p < nparts; p += 64) wsum += exp2f(lse[p] - mx);
+  wsum = li_wave_sum(wsum);
 
   float acc[kMaxC];
 #pragma unroll
   for (int c = 0; c < kMaxC; ++c) acc[c] = 0.f;
-  float wsum = 0.f;
-  for (int p = 0; p < nparts; ++p) {
-    const float w = exp2f(lse[p] - mx);
-    wsum += w;
+  for (int p0 = 0; p0 < nparts; p0 += 64) {
+    const float wl = (p0 + lane < nparts) ? exp2f(lse[p0 + lane] - mx) : 0.f;
+    const int pend = min(64, nparts - p0);
+    for (int pb = 0; pb < pend; pb += kBatch) {
+      float v[kBatch][kMaxC];
 #pragma unroll
-    for (int c = 0; c < kMaxC; ++c) {
-      const int d = lane + 64 * c;
-      if (d < D) acc[c] = fmaf(w, po[(int64_t)p * D + d], acc[c]);
+      for (int k = 0; k < kBatch; ++k) {
+        const int p = p0 + pb + k;
+#pragma unroll
+        for (int c = 0; c < kMaxC; ++c) {
+          const int d = lane + 64 * c;
+          v[k][c] = (pb + k < pend && d < D) ? po[(int64_t)p * D + d] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const float w = __shfl(wl, (pb + k) & 63, 64);
+#pragma unroll
+        for (int c = 0; c < kMaxC; ++c) acc[c] = fmaf(w, v[k][c], acc[c]);
+      }
     }
   }
   const float inv = 1.f / wsum;

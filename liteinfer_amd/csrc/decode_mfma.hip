@@ -4,31 +4,37 @@
 // paged_kernels.py:374-413, :462-571): per (sequence, KV head, partition),
 // the G query heads sharing a KV head fold the partition's keys into an
 // online softmax, fp32 throughout, weights rounded to the value dtype before
-// they multiply V. The work is laid out for v_mfma_f32_16x16x32_{bf16,f16}
-// and for 16-byte loads straight from the pool:
+// they multiply V. One wave64 per partition, 32 keys per step, laid out for
+// v_mfma_f32_16x16x32_{bf16,f16}. Lane (n, g) = (lane % 16, lane / 16).
 //
-//   S^T = K Q^T     A = K rows (16 keys x 32 dims), B = Q^T (32 dims x 16
-//                   heads). Lane (n, g) = (lane % 16, lane / 16) holds 8 dims
-//                   of key n and the same 8 dims of head n; the result gives
-//                   lane (n, g) the scores of keys 4g..4g+3 for head n.
+// Loads. Lane (n, g) loads 16 bytes (dims 8n..8n+7) of K and of V for each of
+// the 8 keys kappa(g, 0..7) = {4g..4g+3, 16+4g..16+4g+3} of the tile, so each
+// load instruction reads 4 whole 256-byte pool rows, 16 lanes per row. (A
+// layout where 16 lanes each read 64 bytes of 16 different rows measured 20%
+// less HBM bandwidth.) The next tile's loads are always in flight while the
+// current one is folded.
+//
+//   S^T = K Q^T     A = K (16 keys x 32 dims), B = Q^T (32 dims x 16 heads).
+//                   The A operand wants lane (m, g) to hold 8 dims of key m,
+//                   so K goes through LDS once: rows written as loaded, read
+//                   back at dims 32j + 8g (rows padded to 272 bytes, so 16
+//                   lanes reading 16 rows hit 16 distinct bank groups). The
+//                   result gives lane (n, g) the scores of keys 4g..4g+3 (and
+//                   16+4g.. from the second block) for head n.
 //   O^T += V^T P^T  A = V^T (16 rows x 32 keys), B = P^T (32 keys x 16 heads).
-//                   Two S^T blocks give lane (n, g) the 8 weights of keys
-//                   {4g..4g+3, 16+4g..16+4g+3} for head n: exactly its B
-//                   operand, with no lane exchange. For the A operand lane
-//                   (n, g) loads 16 bytes (dims 8n..8n+7) of each of those 8
-//                   keys, so 16 lanes cover one 256-byte pool row per load
-//                   instruction, and a register-only 8x8 transpose turns them
-//                   into 8 A operands, one per dim within the chunk: row n of
-//                   instruction i is dim 8n + i.
+//                   Lane (n, g)'s 8 weights are for keys kappa(g, 0..7) of
+//                   head n: exactly its B operand, no lane exchange. Its 8
+//                   V chunks (8 keys x dims 8n..8n+7) become 8 A operands by
+//                   a register-only 8x8 transpose: row n of instruction i is
+//                   dim 8n + i.
 //   The result gives lane (n, g) dims {8(4g+r) + i} of head n, so the
 //   running-max rescale is per lane (its own head) and nothing is reduced
 //   across lanes except the tile maximum (two xor shuffles) and, once at the
 //   end, the denominator.
 //
 // Heads past G are zero rows of Q^T: they score 0 and are never stored.
-// Keys past the partition's end are clamped to its last key for the load and
-// masked to -inf for the softmax, so every load is in bounds. One wave64 per
-// partition; the next 32-key tile is loaded while the current one is folded.
+// Keys past the partition's end read the last key's slot (a real row) and
+// are masked to -inf, so every load is in bounds.
 #include "li_attention.h"
 
 namespace li {
@@ -55,36 +61,44 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T, int D>
 struct DecodeTile {
-  using Frag = typename Mfma<T>::Frag;
-  Frag k0[D / 32];  // key n of the tile, dims 32j + 8g ..
-  Frag k1[D / 32];  // key 16 + n
-  u32x4_t v[8];     // dims 8n.. of key kappa(g, e)
+  u32x4_t k[8];  // dims 8n.. of key kappa(g, e)
+  u32x4_t v[8];
 };
 
-// Key of the tile whose weight lane group g holds in B-operand slot e.
+// Key of the tile whose K/V chunk and weight lane group g holds in slot e.
 __device__ __forceinline__ int kappa(int g, int e) { return (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4)); }
 
+// Keys whose slots are staged in LDS at a time. A partition chosen by the
+// policy is at most this long, so it is one chunk; a pinned split count can
+// make longer partitions, which take several.
+constexpr int kSlotChunk = 512;
+
+// LDS row pitch of the K tile, in elements: 128 dims + 8 of padding.
+constexpr int kKPitch = 136;
+
+template <typename T>
+__device__ __forceinline__ u32x4_t load16_stream(const T* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+}
+
+// Issues the 16 loads of the 32-key tile whose first key is entry `t` of the
+// staged slots.
 template <typename T, int D>
 __device__ __forceinline__ void load_tile(DecodeTile<T, D>& tl, const T* __restrict__ kpool,
-                                          const T* __restrict__ vpool, const int64_t* __restrict__ srow,
-                                          int64_t p_s0, int t0, int ke, int n, int g) {
-  using Frag = typename Mfma<T>::Frag;
+                                          const T* __restrict__ vpool, const int* __restrict__ sl,
+                                          int64_t p_s0, int t, int n, int g) {
   constexpr int kChunks = D / 8;
-  const int64_t s0 = srow[min(t0 + n, ke - 1)];
-  const int64_t s1 = srow[min(t0 + 16 + n, ke - 1)];
-  const T* r0 = kpool + s0 * p_s0 + 8 * g;
-  const T* r1 = kpool + s1 * p_s0 + 8 * g;
-#pragma unroll
-  for (int j = 0; j < D / 32; ++j) {
-    tl.k0[j] = *reinterpret_cast<const Frag*>(r0 + 32 * j);
-    tl.k1[j] = *reinterpret_cast<const Frag*>(r1 + 32 * j);
-  }
+  const int4 sa = *reinterpret_cast<const int4*>(sl + t + 4 * g);
+  const int4 sb = *reinterpret_cast<const int4*>(sl + t + 16 + 4 * g);
+  const int vs[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int64_t sv = srow[min(t0 + kappa(g, e), ke - 1)];
+    const int64_t off = (int64_t)vs[e] * p_s0 + 8 * n;
     if (n < kChunks) {
-      tl.v[e] = *reinterpret_cast<const u32x4_t*>(vpool + sv * p_s0 + 8 * n);
+      tl.k[e] = load16_stream(kpool + off);
+      tl.v[e] = load16_stream(vpool + off);
     } else {
+      tl.k[e] = u32x4_t{0u, 0u, 0u, 0u};
       tl.v[e] = u32x4_t{0u, 0u, 0u, 0u};
     }
   }
@@ -96,14 +110,19 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
   using Frag = typename M::Frag;
   constexpr int kSteps = D / 32;
   constexpr int kChunks = D / 8;
+  __shared__ __attribute__((aligned(16))) int sl[kSlotChunk + 64];
+  __shared__ __attribute__((aligned(16))) T kt[32 * kKPitch];
 
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
+  // Partition-major order: every sequence's first partition is dispatched
+  // before any second one, so the grid's empty tail (partitions past a short
+  // context) comes last and exits at once.
   int bid = blockIdx.x;
-  const int part = bid % a.num_parts;
-  bid /= a.num_parts;
   const int kvh = bid % a.num_kv_heads;
-  const int seq = bid / a.num_kv_heads;
+  bid /= a.num_kv_heads;
+  const int seq = bid % a.batch;
+  const int part = bid / a.batch;
 
   const int ctx = a.ctx[seq];
   const int plen = a.part_len > 0 ? a.part_len : max(1, (ctx + a.num_parts - 1) / a.num_parts);
@@ -138,18 +157,26 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  DecodeTile<T, D> cur, nxt;
-  load_tile<T, D>(cur, kpool, vpool, srow, a.p_s0, kb, ke, n, g);
-
-  for (int t0 = kb; t0 < ke; t0 += 32) {
-    const bool more = t0 + 32 < ke;
-    if (more) load_tile<T, D>(nxt, kpool, vpool, srow, a.p_s0, t0 + 32, ke, n, g);
-
+  // Folds the tile whose data is in `tl` (first key t0, chunk end c1).
+  auto fold = [&](const DecodeTile<T, D>& tl, int t0, int c1) {
+    // K rows into LDS as loaded, then back out in the MFMA A layout.
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (n < kChunks) *reinterpret_cast<u32x4_t*>(kt + kappa(g, e) * kKPitch + 8 * n) = tl.k[e];
+    }
+    __syncthreads();
+    Frag k0[kSteps], k1[kSteps];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      k0[j] = *reinterpret_cast<const Frag*>(kt + n * kKPitch + 32 * j + 8 * g);
+      k1[j] = *reinterpret_cast<const Frag*>(kt + (16 + n) * kKPitch + 32 * j + 8 * g);
+    }
+    __syncthreads();
     floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < kSteps; ++j) {
-      s0 = M::mma(cur.k0[j], qf[j], s0);
-      s1 = M::mma(cur.k1[j], qf[j], s1);
+      s0 = M::mma(k0[j], qf[j], s0);
+      s1 = M::mma(k1[j], qf[j], s1);
     }
     float x[8];
 #pragma unroll
@@ -160,7 +187,7 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
     float mx = -INFINITY;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      x[e] = (t0 + kappa(g, e) < ke) ? x[e] * sc : -INFINITY;
+      x[e] = (t0 + kappa(g, e) < c1) ? x[e] * sc : -INFINITY;
       mx = fmaxf(mx, x[e]);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -179,14 +206,13 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
     const Frag pf = __builtin_bit_cast(Frag, pw);
-
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int w = i >> 1;
       u32x4_t va;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const uint32_t lo = cur.v[2 * u][w], hi = cur.v[2 * u + 1][w];
+        const uint32_t lo = tl.v[2 * u][w], hi = tl.v[2 * u + 1][w];
         va[u] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
       }
 #pragma unroll
@@ -194,7 +220,40 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
       acc[i] = M::mma(__builtin_bit_cast(Frag, va), pf, acc[i]);
     }
     m = mnew;
-    if (more) cur = nxt;
+  };
+
+  DecodeTile<T, D> ta, tb;
+  for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
+    const int c1 = min(c0 + kSlotChunk, ke);
+    // Stage this chunk's slots (int32: a pool holds fewer than 2^31 slots),
+    // plus one tile past its end. Entries past the chunk repeat its last
+    // slot, so the loads of a partial or a look-ahead tile read real rows
+    // (and hit the cache); their scores are masked.
+    __syncthreads();
+    int vals[kSlotChunk / 64 + 1];
+#pragma unroll
+    for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
+#pragma unroll
+    for (int k = 0; k < kSlotChunk / 64 + 1; ++k) sl[lane + 64 * k] = vals[k];
+    __syncthreads();
+
+    // Double-buffered: the next tile's loads are always in flight while the
+    // current one is folded, and no load sits under a branch, so the wait
+    // before each fold covers only the tile it folds.
+    const int len = c1 - c0;
+    load_tile<T, D>(ta, kpool, vpool, sl, a.p_s0, 0, n, g);
+    for (int t = 0;;) {
+      load_tile<T, D>(tb, kpool, vpool, sl, a.p_s0, min(t + 32, kSlotChunk), n, g);
+      __builtin_amdgcn_sched_barrier(0);  // keep the look-ahead loads ahead of the fold
+      fold(ta, c0 + t, c1);
+      t += 32;
+      if (t >= len) break;
+      load_tile<T, D>(ta, kpool, vpool, sl, a.p_s0, min(t + 32, kSlotChunk), n, g);
+      __builtin_amdgcn_sched_barrier(0);
+      fold(tb, c0 + t, c1);
+      t += 32;
+      if (t >= len) break;
+    }
   }
 
   float lt = l + __shfl_xor(l, 16, 64);
