@@ -37,6 +37,8 @@
 // are masked to -inf, so every load is in bounds.
 #include "li_attention.h"
 
+#include <cstdlib>
+
 namespace li {
 namespace {
 
@@ -59,59 +61,106 @@ struct Mfma<li_f16> {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <typename T, int D>
-struct DecodeTile {
-  u32x4_t k[8];  // dims 8n.. of key kappa(g, e)
-  u32x4_t v[8];
-};
-
-// Key of the tile whose K/V chunk and weight lane group g holds in slot e.
+// Key of the tile whose weight lane group g holds in B-operand slot e (the
+// order the S^T blocks deliver scores in).
 __device__ __forceinline__ int kappa(int g, int e) { return (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4)); }
 
 // Keys whose slots are staged in LDS at a time. A partition chosen by the
 // policy is at most this long, so it is one chunk; a pinned split count can
 // make longer partitions, which take several.
-constexpr int kSlotChunk = 512;
+constexpr int kSlotChunk = 1024;
 
-// LDS row pitch of the K tile, in elements: 128 dims + 8 of padding.
-constexpr int kKPitch = 136;
+// LDS tile layout. A tile is 32 keys; K rows then V rows, D / 8 chunks of 16
+// bytes per row. A load instruction writes lane L's 16 bytes at 16 L, so with
+// CH = D / 8 chunks per row one instruction fills 64 / CH rows; instruction i,
+// row-in-instruction rr holds key rr * (CH / 2) + i (so each lane's keys are
+// consecutive), and chunk c of key k sits in slot c ^ (k % CH) of its row, so
+// 16 lanes reading the same chunk of 16 keys hit 16 distinct bank groups.
+template <int D>
+struct TileLayout {
+  static constexpr int kCh = D / 8;             // 16-byte chunks per row
+  static constexpr int kRowsPerInst = 64 / kCh;  // rows one load instruction fills
+  static constexpr int kInsts = 32 / kRowsPerInst;
+  static constexpr int kRowBytes = D * 2;
+  static constexpr int kTileBytes = 2 * 32 * kRowBytes;  // K then V
+  __device__ static int row_of(int key) { return kRowsPerInst * (key % kInsts) + key / kInsts; }
+  __device__ static int offset(int key, int chunk) {  // byte offset within the K (or V) half
+    return row_of(key) * kRowBytes + 16 * (chunk ^ (key % kCh));
+  }
+};
 
-template <typename T>
-__device__ __forceinline__ u32x4_t load16_stream(const T* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+// One direct-to-LDS load: every lane's 16 bytes at `g` land at lds + 16 * lane.
+//
+// Written as inline assembly on purpose: the compiler models the builtin's
+// LDS write conservatively and waits for every such load to land before any
+// LDS read, which would serialise the two stages. Here the kernel counts the
+// loads itself (li_wait_vm below) and the "memory" clobbers keep every other
+// memory access in program order around them.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(g)
+      : "memory");
 }
 
-// Issues the 16 loads of the 32-key tile whose first key is entry `t` of the
-// staged slots.
+// Waits until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void li_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(p);
+}
+
+// Issues the 2 * kInsts direct-to-LDS loads of the 32-key tile whose first
+// key is entry `t` of the staged slots, into the stage at `stage`. Lane
+// (rr, n) = (lane / CH, lane % CH) loads keys rr * kInsts + i.
 template <typename T, int D>
-__device__ __forceinline__ void load_tile(DecodeTile<T, D>& tl, const T* __restrict__ kpool,
-                                          const T* __restrict__ vpool, const int* __restrict__ sl,
-                                          int64_t p_s0, int t, int n, int g) {
-  constexpr int kChunks = D / 8;
-  const int4 sa = *reinterpret_cast<const int4*>(sl + t + 4 * g);
-  const int4 sb = *reinterpret_cast<const int4*>(sl + t + 16 + 4 * g);
-  const int vs[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+__device__ __forceinline__ void issue_tile(char* stage, const T* __restrict__ kpool, const T* __restrict__ vpool,
+                                           const int* __restrict__ sl, int64_t p_s0, int t, int lane) {
+  using L = TileLayout<D>;
+  const int rr = lane / L::kCh, nn = lane % L::kCh;
+  int keys[L::kInsts];
+  if constexpr (L::kInsts == 8) {
+    const int4 a = *reinterpret_cast<const int4*>(sl + t + 8 * rr);
+    const int4 b = *reinterpret_cast<const int4*>(sl + t + 8 * rr + 4);
+    keys[0] = a.x; keys[1] = a.y; keys[2] = a.z; keys[3] = a.w;
+    keys[4] = b.x; keys[5] = b.y; keys[6] = b.z; keys[7] = b.w;
+  } else {
+    const int4 a = *reinterpret_cast<const int4*>(sl + t + 4 * rr);
+    keys[0] = a.x; keys[1] = a.y; keys[2] = a.z; keys[3] = a.w;
+  }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int64_t off = (int64_t)vs[e] * p_s0 + 8 * n;
-    if (n < kChunks) {
-      tl.k[e] = load16_stream(kpool + off);
-      tl.v[e] = load16_stream(vpool + off);
-    } else {
-      tl.k[e] = u32x4_t{0u, 0u, 0u, 0u};
-      tl.v[e] = u32x4_t{0u, 0u, 0u, 0u};
-    }
+  for (int i = 0; i < L::kInsts; ++i) {
+    const int key = rr * L::kInsts + i;
+    const int chunk = nn ^ (key % L::kCh);
+    const int64_t off = (int64_t)keys[i] * p_s0 + 8 * chunk;
+    const uint32_t dst = lds_addr(stage + i * 1024);  // rows kRowsPerInst * i ..: 1 KiB per instruction
+    dma16(kpool + off, dst);
+    dma16(vpool + off, dst + 32 * L::kRowBytes);
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int kStages>
 __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
+  using L = TileLayout<D>;
   constexpr int kSteps = D / 32;
   constexpr int kChunks = D / 8;
   __shared__ __attribute__((aligned(16))) int sl[kSlotChunk + 64];
-  __shared__ __attribute__((aligned(16))) T kt[32 * kKPitch];
+  // Two stages as separate LDS objects, so the compiler can tell a read of
+  // one from the direct-to-LDS loads still landing in the other.
+  __shared__ __attribute__((aligned(1024))) char stage0[L::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char stage1[L::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char stage2[kStages == 3 ? L::kTileBytes : 16];
 
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
@@ -157,103 +206,111 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Folds the tile whose data is in `tl` (first key t0, chunk end c1).
-  auto fold = [&](const DecodeTile<T, D>& tl, int t0, int c1) {
-    // K rows into LDS as loaded, then back out in the MFMA A layout.
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      if (n < kChunks) *reinterpret_cast<u32x4_t*>(kt + kappa(g, e) * kKPitch + 8 * n) = tl.k[e];
-    }
-    __syncthreads();
-    Frag k0[kSteps], k1[kSteps];
-#pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
-      k0[j] = *reinterpret_cast<const Frag*>(kt + n * kKPitch + 32 * j + 8 * g);
-      k1[j] = *reinterpret_cast<const Frag*>(kt + (16 + n) * kKPitch + 32 * j + 8 * g);
-    }
-    __syncthreads();
-    floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
-      s0 = M::mma(k0[j], qf[j], s0);
-      s1 = M::mma(k1[j], qf[j], s1);
-    }
-    float x[8];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      x[r] = s0[r];
-      x[4 + r] = s1[r];
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[e] = (t0 + kappa(g, e) < c1) ? x[e] * sc : -INFINITY;
-      mx = fmaxf(mx, x[e]);
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mnew = fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-    float psum = 0.f;
-    float p[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p[e] = __builtin_amdgcn_exp2f(x[e] - mnew);
-      psum += p[e];
-    }
-    l = l * alpha + psum;
-    u32x4_t pw;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
-    const Frag pf = __builtin_bit_cast(Frag, pw);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int w = i >> 1;
-      u32x4_t va;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const uint32_t lo = tl.v[2 * u][w], hi = tl.v[2 * u + 1][w];
-        va[u] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[i][r] *= alpha;
-      acc[i] = M::mma(__builtin_bit_cast(Frag, va), pf, acc[i]);
-    }
-    m = mnew;
-  };
-
-  DecodeTile<T, D> ta, tb;
   for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
     const int c1 = min(c0 + kSlotChunk, ke);
+    const int len = c1 - c0;
+    const int ntiles = (len + 31) / 32;
     // Stage this chunk's slots (int32: a pool holds fewer than 2^31 slots),
-    // plus one tile past its end. Entries past the chunk repeat its last
-    // slot, so the loads of a partial or a look-ahead tile read real rows
-    // (and hit the cache); their scores are masked.
+    // plus two tiles past its end. Entries past the chunk repeat its last
+    // slot, so the loads of a partial tile read real rows; their scores are
+    // masked.
     __syncthreads();
-    int vals[kSlotChunk / 64 + 1];
+    {
+      int vals[kSlotChunk / 64 + 1];
 #pragma unroll
-    for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
+      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
 #pragma unroll
-    for (int k = 0; k < kSlotChunk / 64 + 1; ++k) sl[lane + 64 * k] = vals[k];
+      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) sl[lane + 64 * k] = vals[k];
+    }
     __syncthreads();
 
-    // Double-buffered: the next tile's loads are always in flight while the
-    // current one is folded, and no load sits under a branch, so the wait
-    // before each fold covers only the tile it folds.
-    const int len = c1 - c0;
-    load_tile<T, D>(ta, kpool, vpool, sl, a.p_s0, 0, n, g);
-    for (int t = 0;;) {
-      load_tile<T, D>(tb, kpool, vpool, sl, a.p_s0, min(t + 32, kSlotChunk), n, g);
-      __builtin_amdgcn_sched_barrier(0);  // keep the look-ahead loads ahead of the fold
-      fold(ta, c0 + t, c1);
-      t += 32;
-      if (t >= len) break;
-      load_tile<T, D>(ta, kpool, vpool, sl, a.p_s0, min(t + 32, kSlotChunk), n, g);
-      __builtin_amdgcn_sched_barrier(0);
-      fold(tb, c0 + t, c1);
-      t += 32;
-      if (t >= len) break;
+    // Folds the tile in `stage` whose first key is t0.
+    auto fold = [&](const char* stage, int t0) {
+      const char* vstage = stage + 32 * L::kRowBytes;
+      floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < kSteps; ++j) {
+        const Frag k0 = *reinterpret_cast<const Frag*>(stage + L::offset(n, 4 * j + g));
+        const Frag k1 = *reinterpret_cast<const Frag*>(stage + L::offset(16 + n, 4 * j + g));
+        s0 = M::mma(k0, qf[j], s0);
+        s1 = M::mma(k1, qf[j], s1);
+      }
+      u32x4_t vr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vr[e] = (n < kChunks) ? *reinterpret_cast<const u32x4_t*>(vstage + L::offset(kappa(g, e), n))
+                              : u32x4_t{0u, 0u, 0u, 0u};
+      }
+      float x[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = s0[r];
+        x[4 + r] = s1[r];
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = (t0 + kappa(g, e) < c1) ? x[e] * sc : -INFINITY;
+        mx = fmaxf(mx, x[e]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mnew = fmaxf(m, mx);
+      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      float psum = 0.f;
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(x[e] - mnew);
+        psum += p[e];
+      }
+      l = l * alpha + psum;
+      u32x4_t pw;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
+      const Frag pf = __builtin_bit_cast(Frag, pw);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int w = i >> 1;
+        u32x4_t va;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t lo = vr[2 * u][w], hi = vr[2 * u + 1][w];
+          va[u] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][r] *= alpha;
+        acc[i] = M::mma(__builtin_bit_cast(Frag, va), pf, acc[i]);
+      }
+      m = mnew;
+    };
+
+    // kStages stages: while one tile is folded the next kStages - 1 tiles'
+    // loads land in the others. Past the chunk the look-ahead re-reads a real
+    // tile (cache hits), so the loads in flight are the same every step and
+    // no load sits under a branch.
+    constexpr int kInFlight = 2 * L::kInsts * (kStages - 1);
+    issue_tile<T, D>(stage0, kpool, vpool, sl, a.p_s0, 0, lane);
+    if constexpr (kStages == 3) issue_tile<T, D>(stage1, kpool, vpool, sl, a.p_s0, min(32, kSlotChunk), lane);
+    for (int ti = 0;;) {
+      issue_tile<T, D>(kStages == 3 ? stage2 : stage1, kpool, vpool, sl, a.p_s0,
+                       min(32 * (ti + kStages - 1), kSlotChunk), lane);
+      li_wait_vm<kInFlight>();
+      fold(stage0, c0 + 32 * ti);
+      if (++ti >= ntiles) break;
+      issue_tile<T, D>(stage0, kpool, vpool, sl, a.p_s0, min(32 * (ti + kStages - 1), kSlotChunk), lane);
+      li_wait_vm<kInFlight>();
+      fold(stage1, c0 + 32 * ti);
+      if (++ti >= ntiles) break;
+      if constexpr (kStages == 3) {
+        issue_tile<T, D>(stage1, kpool, vpool, sl, a.p_s0, min(32 * (ti + kStages - 1), kSlotChunk), lane);
+        li_wait_vm<kInFlight>();
+        fold(stage2, c0 + 32 * ti);
+        if (++ti >= ntiles) break;
+      }
     }
+    // Drain the look-ahead loads before the slots (and stages) are reused.
+    li_wait_vm<0>();
   }
 
   float lt = l + __shfl_xor(l, 16, 64);
@@ -313,12 +370,20 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
   if (blocks == 0) return LI_OK;
   if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "decode grid of %lld blocks is too large", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(64);
+  static const int stages = [] {
+    const char* v = std::getenv("LI_DECODE_STAGES");
+    return (v && v[0] == '3') ? 3 : 2;
+  }();
   if (dtype == LI_BF16) {
-    if (a.head_dim == 128) hipLaunchKernelGGL((decode_mfma<li_bf16, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((decode_mfma<li_bf16, 64>), grid, block, 0, s, a);
+    if (a.head_dim == 128) {
+      if (stages == 3) hipLaunchKernelGGL((decode_mfma<li_bf16, 128, 3>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((decode_mfma<li_bf16, 128, 2>), grid, block, 0, s, a);
+    } else {
+      hipLaunchKernelGGL((decode_mfma<li_bf16, 64, 2>), grid, block, 0, s, a);
+    }
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((decode_mfma<li_f16, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((decode_mfma<li_f16, 64>), grid, block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((decode_mfma<li_f16, 128, 2>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((decode_mfma<li_f16, 64, 2>), grid, block, 0, s, a);
   }
   return check_launch("decode_mfma");
 }

@@ -19,7 +19,7 @@ namespace {
 // so a long context is cut more finely than a short one and every wave
 // carries about the same bytes whatever the spread of context lengths.
 constexpr int kTargetWavesPerCu = 8;
-constexpr int kMaxPartition = 512;
+constexpr int kMaxPartition = 1024;
 constexpr int kMinTilesToSplit = 4;
 constexpr int kMaxPartitions = 1024;
 constexpr int kDefaultBlockKv = 64;

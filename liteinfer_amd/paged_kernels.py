@@ -78,7 +78,7 @@ def choose_num_splits(
     MI355X, computed by the library (`li_choose_num_splits`) so the Python and
     C callers agree. The unsplit grid is one wave per (sequence, KV head);
     when that cannot keep 256 CUs streaming, each sequence's keys are cut
-    into fixed-length partitions — at most 512 keys each, at least one
+    into fixed-length partitions — at most 1024 keys each, at least one
     `block_kv` tile — until the grid holds about eight waves per CU. A context
     under four tiles is never cut, and a grid that is already full is not
     either. The answer is a function of host integers only (`max_context` is

@@ -63,11 +63,11 @@ def test_a_longer_context_is_cut_more_finely():
     assert _splits(batch=1, kv_heads=8, max_context=4096) > _splits(batch=1, kv_heads=8, max_context=256)
 
 
-def test_partitions_never_exceed_512_keys_so_waves_carry_equal_work():
-    # Llama-3-8B decode at batch 64 over contexts up to 8192: 16 partitions of 512.
-    assert _splits(batch=64, kv_heads=8, max_context=8192) == 16
-    # batch 8 over 131072: 256 partitions of 512.
-    assert _splits(batch=8, kv_heads=8, max_context=131072) == 256
+def test_partitions_never_exceed_1024_keys_so_waves_carry_equal_work():
+    # Llama-3-8B decode at batch 64 over contexts up to 8192: 8 partitions of 1024.
+    assert _splits(batch=64, kv_heads=8, max_context=8192) == 8
+    # batch 8 over 131072: 128 partitions of 1024.
+    assert _splits(batch=8, kv_heads=8, max_context=131072) == 128
 
 
 def _plan(**kw):
