@@ -1,0 +1,94 @@
+// Building blocks shared by the MFMA attention kernels: the 16x16x32 MFMA
+// for bf16 / fp16, the 32-key LDS tile layout filled by direct-to-LDS loads,
+// and explicit vector-memory waits.
+#pragma once
+
+#include "li_common.h"
+
+namespace li {
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<li_bf16> {
+  using Frag = bf16x8_t;
+  static __device__ __forceinline__ floatx4_t mma(Frag a, Frag b, floatx4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<li_f16> {
+  using Frag = f16x8_t;
+  static __device__ __forceinline__ floatx4_t mma(Frag a, Frag b, floatx4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Key of the tile whose weight lane group g holds in B-operand slot e (the
+// order the S^T blocks deliver scores in).
+__device__ __forceinline__ int kappa(int g, int e) { return (e < 4 ? 4 * g + e : 16 + 4 * g + (e - 4)); }
+
+// Keys whose slots are staged in LDS at a time. A partition chosen by the
+// policy is at most this long, so it is one chunk; a pinned split count can
+// make longer partitions, which take several.
+constexpr int kSlotChunk = 1024;
+
+// LDS tile layout. A tile is 32 keys; K rows then V rows, D / 8 chunks of 16
+// bytes per row. A load instruction writes lane L's 16 bytes at 16 L, so with
+// CH = D / 8 chunks per row one instruction fills 64 / CH rows; instruction i,
+// row-in-instruction rr holds key rr * (CH / 2) + i (so each lane's keys are
+// consecutive), and chunk c of key k sits in slot c ^ (k % CH) of its row, so
+// 16 lanes reading the same chunk of 16 keys hit 16 distinct bank groups.
+template <int D>
+struct TileLayout {
+  static constexpr int kCh = D / 8;             // 16-byte chunks per row
+  static constexpr int kRowsPerInst = 64 / kCh;  // rows one load instruction fills
+  static constexpr int kInsts = 32 / kRowsPerInst;
+  static constexpr int kRowBytes = D * 2;
+  static constexpr int kTileBytes = 2 * 32 * kRowBytes;  // K then V
+  __device__ static int row_of(int key) { return kRowsPerInst * (key % kInsts) + key / kInsts; }
+  __device__ static int offset(int key, int chunk) {  // byte offset within the K (or V) half
+    return row_of(key) * kRowBytes + 16 * (chunk ^ (key % kCh));
+  }
+};
+
+// One direct-to-LDS load: every lane's 16 bytes at `g` land at lds + 16 * lane.
+//
+// Written as inline assembly on purpose: the compiler models the builtin's
+// LDS write conservatively and waits for every such load to land before any
+// LDS read, which would serialise the two stages. Here the kernel counts the
+// loads itself (li_wait_vm below) and the "memory" clobbers keep every other
+// memory access in program order around them.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
+      : "memory");
+}
+
+// Waits until at most N vector-memory operations of this wave are in flight.
+template <int N>
+__device__ __forceinline__ void li_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(p);
+}
+
+constexpr float kLog2eMfma = 1.4426950408889634f;
+
+// A running softmax maximum is only raised when a tile's maximum exceeds it
+// by more than this (in log2 units); until then the weights exp2(s - m) may
+// reach 2^kLazyRescale, which fp32 sums and bf16 / fp16 weights hold without
+// loss of relative precision. Most tiles then skip rescaling the
+// accumulator.
+constexpr float kLazyRescale = 8.0f;
+
+}  // namespace li

@@ -1,12 +1,317 @@
-// Packed / chunked prefill on CDNA4 matrix cores.
+// Packed / chunked prefill on CDNA4 matrix cores (bf16 / fp16, head_dim 64 or
+// 128, up to 16 query heads per KV head).
+//
+// Same attention as liteinfer's prefill kernel (liteinfer/models/
+// paged_kernels.py:416-459 with _attend_query_block, :291-371): a
+// sequence's queries are the last positions of its context, each sees the
+// keys up to its own position, the online softmax runs in fp32 and the
+// weights are rounded to the value dtype before they multiply V.
+//
+// One workgroup of 4 waves per (sequence, KV head, block of 128 / G query
+// tokens). Its 128 rows are (query token, head) pairs, head fastest, so the G
+// heads that share a KV head read each K/V tile once; wave w owns rows
+// 32w..32w+31 as two 16-row MFMA blocks. The keys [0, last query's
+// position] stream through LDS 64 at a time, loaded straight into LDS by all
+// four waves (two stages, so the next 64 keys land while these are folded),
+// in the 32-key tile layout the decode kernel uses (li_mfma.h). Per 32 keys
+// and 16 rows:
+//
+//   S^T = K Q^T     A = K rows from LDS, B = the rows' Q^T kept in registers.
+//                   Lane (n, g) gets the scores of keys {4g..4g+3,
+//                   16+4g..16+4g+3} for row n.
+//   O^T += V^T P^T  B = P^T is those 8 weights as they are; A = V^T is 8
+//                   16-byte V chunks (dims 8n.., the same 8 keys) from LDS
+//                   turned into 8 operands by a register-only 8x8 transpose,
+//                   shared by both row blocks.
+//
+// A row's visibility is key <= its position; the mask is a compare per
+// score, applied on every tile (it is all-true before the block's first
+// query). Padding rows (past the block or the sequence) see every key with a
+// zero query, so they stay finite, and are never stored.
+//
+// Grid order: the (sequence, KV head) pair is the fastest index, so with
+// num_kv_heads a multiple of 8 every query block of a pair lands on the same
+// XCD (work-groups are dealt to the 8 XCDs round robin) and reuses its K/V
+// from that XCD's L2; the last query blocks, which see the most keys, are
+// dispatched first.
 #include "li_attention.h"
+#include "li_mfma.h"
 
 namespace li {
+namespace {
 
-bool prefill_mfma_applies(const AttnArgs&, int) { return false; }
+constexpr int kWaves = 4;
+constexpr int kRows = 128;  // (query, head) rows per work-group
+constexpr int kStageKeys = 64;
 
-int launch_prefill_mfma(const AttnArgs&, int, hipStream_t) {
-  return fail(LI_EUNSUPPORTED, "prefill MFMA kernel is not built");
+// Issues this wave's share of the direct-to-LDS loads of the 64 keys whose
+// first key is entry `t` of the staged slots: of each 32-key half, the
+// instructions i = w * kInsts / 4 + ... (K and V).
+template <typename T, int D>
+__device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ kpool, const T* __restrict__ vpool,
+                                            const int* __restrict__ sl, int64_t p_s0, int t, int lane, int w) {
+  using L = TileLayout<D>;
+  constexpr int kPerWave = L::kInsts / kWaves;
+  const int rr = lane / L::kCh, nn = lane % L::kCh;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    char* tile = stage + half * L::kTileBytes;
+#pragma unroll
+    for (int ii = 0; ii < kPerWave; ++ii) {
+      const int i = w * kPerWave + ii;
+      const int key = rr * L::kInsts + i;
+      const int slot = sl[t + 32 * half + key];
+      const int chunk = nn ^ (key % L::kCh);
+      const int64_t off = (int64_t)slot * p_s0 + 8 * chunk;
+      const uint32_t dst = lds_addr(tile + i * 1024);
+      dma16(kpool + off, dst);
+      dma16(vpool + off, dst + 32 * L::kRowBytes);
+    }
+  }
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma(AttnArgs a) {
+  using M = Mfma<T>;
+  using Frag = typename M::Frag;
+  using L = TileLayout<D>;
+  constexpr int kSteps = D / 32;
+  constexpr int kChunks = D / 8;
+  constexpr int kDmaPerStage = 2 * 2 * (L::kInsts / kWaves);
+  __shared__ __attribute__((aligned(16))) int sl[kSlotChunk + kStageKeys];
+  __shared__ __attribute__((aligned(1024))) char stages[2][2 * L::kTileBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
+  const int n = lane & 15, g = lane >> 4;
+
+  const int pairs = a.batch * a.num_kv_heads;
+  const int pair = blockIdx.x % pairs;
+  const int qblock = a.num_qblocks - 1 - (int)(blockIdx.x / pairs);
+  const int seq = pair / a.num_kv_heads;
+  const int kvh = pair % a.num_kv_heads;
+
+  const int first_tok = a.qsl[seq];
+  const int nq = a.qsl[seq + 1] - first_tok;
+  const int bq = a.block_q;  // query tokens per block = kRows / groups
+  const int q0 = qblock * bq;
+  if (q0 >= nq) return;
+  const int q1 = min(q0 + bq, nq);
+  const int ctx = a.ctx[seq];
+  const int pos0 = ctx - nq;   // position of the sequence's first query
+  const int kend = pos0 + q1;  // keys this block reads: [0, kend)
+  const int G = a.groups;
+
+  // This lane's two rows (one per 16-row block).
+  int pos[2];
+  bool real[2];
+  int tok[2], head[2];
+  Frag qf[2][kSteps];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int row = 32 * w + 16 * nb + n;
+    const int ql = row / G;
+    real[nb] = row < bq * G && q0 + ql < nq;
+    pos[nb] = real[nb] ? pos0 + q0 + ql : kend;
+    tok[nb] = first_tok + q0 + ql;
+    head[nb] = kvh * G + row % G;
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)tok[nb] * a.q_s0 + (int64_t)head[nb] * a.q_s1 + 8 * g;
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      if (real[nb]) {
+        qf[nb][j] = *reinterpret_cast<const Frag*>(qrow + 32 * j);
+      } else {
+        qf[nb][j] = Frag{};
+      }
+    }
+  }
+
+  // Last key each row sees: its own position (padding rows: the block's last key).
+  const int lim[2] = {min(pos[0], kend - 1), min(pos[1], kend - 1)};
+
+  const T* kpool = static_cast<const T*>(a.kp) + (int64_t)kvh * a.p_s1;
+  const T* vpool = static_cast<const T*>(a.vp) + (int64_t)kvh * a.p_s1;
+  const int64_t* srow = a.st + (int64_t)seq * a.st_s;
+  const float sc = a.scale * kLog2eMfma;
+
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  floatx4_t acc[2][8];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[nb][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Folds the 32 keys of `tile` whose first key is t0 into both row blocks.
+  auto fold = [&](const char* tile, int t0) {
+    const char* vtile = tile + 32 * L::kRowBytes;
+    // S^T, one 16-key block at a time so only its K operands are live.
+    floatx4_t s[2][2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      Frag kf[kSteps];
+#pragma unroll
+      for (int j = 0; j < kSteps; ++j) kf[j] = *reinterpret_cast<const Frag*>(tile + L::offset(16 * b + n, 4 * j + g));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        s[nb][b] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j) s[nb][b] = M::mma(kf[j], qf[nb][j], s[nb][b]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Online softmax per row block; the scale is folded into the exponent.
+    Frag pf[2];
+    float alpha[2];
+    bool rescale = false;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      float x[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = s[nb][0][r];
+        x[4 + r] = s[nb][1][r];
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] = (t0 + kappa(g, e) <= lim[nb]) ? x[e] : -INFINITY;
+        mx = fmaxf(mx, x[e]);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx *= sc;
+      // Lazy rescale: the running maximum only moves when a tile beats it by
+      // more than kLazyRescale (log2 units), so most tiles leave the
+      // accumulator alone; the weights are then at most 2^kLazyRescale.
+      const float mnew = (mx > m[nb] + kLazyRescale) ? mx : m[nb];
+      alpha[nb] = __builtin_amdgcn_exp2f(m[nb] - mnew);
+      rescale |= mnew != m[nb];
+      float psum = 0.f, p[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
+        psum += p[e];
+      }
+      l[nb] = l[nb] * alpha[nb] + psum;
+      m[nb] = mnew;
+      u32x4_t pw;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
+      pf[nb] = __builtin_bit_cast(Frag, pw);
+    }
+    if (__any(rescale)) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[nb][i][r] *= alpha[nb];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // O^T += V^T P^T, four dims of the chunk at a time.
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      // Bytes 8 * half .. of each key's 16-byte chunk: dims 8n + 4 half ..
+      uint2 vr[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vr[e] = (n < kChunks) ? *reinterpret_cast<const uint2*>(vtile + L::offset(kappa(g, e), n) + 8 * half)
+                              : uint2{0u, 0u};
+      }
+#pragma unroll
+      for (int i = 4 * half; i < 4 * half + 4; ++i) {
+        const int wd = (i >> 1) & 1;
+        u32x4_t va;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t lo = wd ? vr[2 * u].y : vr[2 * u].x, hi = wd ? vr[2 * u + 1].y : vr[2 * u + 1].x;
+          va[u] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+        const Frag vf = __builtin_bit_cast(Frag, va);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[nb][i] = M::mma(vf, pf[nb], acc[nb][i]);
+      }
+    }
+  };
+
+  for (int c0 = 0; c0 < kend; c0 += kSlotChunk) {
+    const int c1 = min(c0 + kSlotChunk, kend);
+    const int ntiles = (c1 - c0 + kStageKeys - 1) / kStageKeys;
+    // Stage this chunk's slots plus one stage past its end; entries past the
+    // chunk repeat its last slot so every load reads a real row.
+    __syncthreads();
+    for (int i = tid; i < kSlotChunk + kStageKeys; i += 256) sl[i] = (int)srow[min(c0 + i, c1 - 1)];
+    __syncthreads();
+
+    // Two stages: the next 64 keys land in one while the other is folded.
+    // Past the chunk the look-ahead re-reads a real stage (cache hits), so
+    // every wave has the same loads in flight at every wait.
+    issue_stage<T, D>(stages[0], kpool, vpool, sl, a.p_s0, 0, lane, w);
+    for (int ti = 0; ti < ntiles; ++ti) {
+      issue_stage<T, D>(stages[(ti + 1) & 1], kpool, vpool, sl, a.p_s0, min(kStageKeys * (ti + 1), kSlotChunk),
+                        lane, w);
+      li_wait_vm<kDmaPerStage>();
+      __syncthreads();
+      const char* stage = stages[ti & 1];
+      fold(stage, c0 + kStageKeys * ti);
+      __builtin_amdgcn_sched_barrier(0);  // one 32-key fold's registers at a time
+      fold(stage + L::kTileBytes, c0 + kStageKeys * ti + 32);
+      __syncthreads();
+    }
+    li_wait_vm<0>();
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    float lt = l[nb] + __shfl_xor(l[nb], 16, 64);
+    lt = lt + __shfl_xor(lt, 32, 64);
+    if (!real[nb]) continue;
+    const float inv = 1.f / lt;
+    T* orow = static_cast<T*>(a.out) + (int64_t)tok[nb] * a.o_s0 + (int64_t)head[nb] * a.o_s1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int chunk = 4 * g + r;
+      if (chunk < kChunks) {
+        u32x4_t wv;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) wv[u] = li_pack2<T>(acc[nb][2 * u][r] * inv, acc[nb][2 * u + 1][r] * inv);
+        *reinterpret_cast<u32x4_t*>(orow + 8 * chunk) = wv;
+      }
+    }
+  }
+}
+
+bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
+  return aligned16(p) && (s0 * esize) % 16 == 0 && (s1 * esize) % 16 == 0;
+}
+
+}  // namespace
+
+bool prefill_mfma_applies(const AttnArgs& a, int dtype) {
+  if (dtype != LI_BF16 && dtype != LI_F16) return false;
+  if (a.head_dim != 64 && a.head_dim != 128) return false;
+  if (a.groups < 1 || a.groups > 16) return false;
+  return rows_aligned(a.q, a.q_s0, a.q_s1, 2) && rows_aligned(a.out, a.o_s0, a.o_s1, 2) &&
+         rows_aligned(a.kp, a.p_s0, a.p_s1, 2) && rows_aligned(a.vp, a.p_s0, a.p_s1, 2);
+}
+
+int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) {
+  AttnArgs a = in;
+  a.block_q = kRows / a.groups;
+  a.num_qblocks = cdiv(a.max_query_len, a.block_q);
+  const int64_t blocks = (int64_t)a.batch * a.num_kv_heads * a.num_qblocks;
+  if (blocks == 0) return LI_OK;
+  if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "prefill grid of %lld blocks is too large", (long long)blocks);
+  const dim3 grid((unsigned)blocks), block(256);
+  if (dtype == LI_BF16) {
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64>), grid, block, 0, s, a);
+  } else {
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64>), grid, block, 0, s, a);
+  }
+  return check_launch("prefill_mfma");
 }
 
 }  // namespace li
