@@ -122,6 +122,18 @@ int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
                     size_t workspace_bytes, int dtype, int flags, void* stream);
 
 /*
+ * Workspace bytes li_paged_prefill needs for a pass of `batch` sequences over
+ * a slot table `max_context` wide on a device of `num_cus` compute units
+ * (0 = ask the current device): partials of its one-query sequences, which
+ * the decode kernel serves with a partitioned key axis. No counterpart in
+ * the reference, whose prefill kernel allocates nothing
+ * (liteinfer/models/paged_kernels.py:867).
+ */
+int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
+                          int head_dim, int max_context, int num_cus,
+                          size_t* workspace_bytes);
+
+/*
  * Packed / chunked prefill. Replaces paged_prefill
  * (liteinfer/models/paged_kernels.py:821-882) and _paged_prefill_kernel
  * (:416-459). Sequence i owns query rows [query_start_loc[i],
@@ -130,20 +142,22 @@ int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
  *   out [total_queries, num_heads, head_dim]  strides (out_stride_tok, out_stride_head, 1)
  * and those queries are the last positions of its context of
  * context_lens[i] keys: query j of n sees keys 0 .. context_lens[i] - n + j.
- * max_query_len sizes the grid and must be >= every sequence's query count.
- * block_q / block_kv are the general-shape kernel's tile sizes (0 = default);
- * the MFMA kernel uses its own.
+ * max_query_len sizes the grid and must be >= every sequence's query count;
+ * max_context is slot_table's width. block_q / block_kv are the
+ * general-shape kernel's tile sizes (0 = default); the MFMA kernels use
+ * their own. `workspace` must hold what li_paged_prefill_plan reports.
  */
 int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                      const void* key_pool, const void* value_pool,
                      int64_t pool_stride_slot, int64_t pool_stride_head,
                      const int64_t* slot_table, int64_t slot_table_stride,
-                     const int32_t* context_lens, const int32_t* query_start_loc,
-                     int batch, int max_query_len, void* out,
-                     int64_t out_stride_tok, int64_t out_stride_head,
-                     int num_heads, int num_kv_heads, int head_dim, float scale,
-                     int block_q, int block_kv, int dtype, int flags,
-                     void* stream);
+                     int max_context, const int32_t* context_lens,
+                     const int32_t* query_start_loc, int batch,
+                     int max_query_len, void* out, int64_t out_stride_tok,
+                     int64_t out_stride_head, int num_heads, int num_kv_heads,
+                     int head_dim, float scale, int block_q, int block_kv,
+                     void* workspace, size_t workspace_bytes, int dtype,
+                     int flags, void* stream);
 
 #ifdef __cplusplus
 }

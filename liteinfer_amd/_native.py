@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "li_choose_num_splits",
     "li_paged_decode_plan",
     "li_paged_decode",
+    "li_paged_prefill_plan",
     "li_paged_prefill",
 )
 
@@ -54,14 +55,15 @@ _SIGNATURES = {
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _p],
     ),
+    "li_paged_prefill_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)]),
     "li_paged_prefill": (
         _i32,
-        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _p, _i32, _i32, _p, _i64, _i64,
-         _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _p],
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _i64,
+         _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _p],
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

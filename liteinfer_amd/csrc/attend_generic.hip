@@ -149,6 +149,11 @@ __global__ __launch_bounds__(64) void combine_parts(AttnArgs a) {
   const int lane = threadIdx.x;
   const int head = blockIdx.x % a.num_heads;
   const int seq = blockIdx.x / a.num_heads;
+  int row = seq;
+  if (a.qsl) {  // a packed pass: only its one-query sequences were partitioned
+    row = a.qsl[seq];
+    if (a.qsl[seq + 1] - row != 1) return;
+  }
   const int ctx = a.ctx[seq];
   const int plen = a.part_len > 0 ? a.part_len : max(1, (ctx + a.num_parts - 1) / a.num_parts);
   const int nparts = (ctx + plen - 1) / plen;
@@ -191,7 +196,7 @@ __global__ __launch_bounds__(64) void combine_parts(AttnArgs a) {
     }
   }
   const float inv = 1.f / wsum;
-  T* orow = static_cast<T*>(a.out) + (int64_t)seq * a.o_s0 + (int64_t)head * a.o_s1;
+  T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head * a.o_s1;
 #pragma unroll
   for (int c = 0; c < kMaxC; ++c) {
     const int d = lane + 64 * c;

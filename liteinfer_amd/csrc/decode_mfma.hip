@@ -65,10 +65,10 @@ __device__ __forceinline__ void issue_tile(char* stage, const T* __restrict__ kp
   for (int i = 0; i < L::kInsts; ++i) {
     const int key = rr * L::kInsts + i;
     const int chunk = nn ^ (key % L::kCh);
-    const int64_t off = (int64_t)keys[i] * p_s0 + 8 * chunk;
     const uint32_t dst = lds_addr(stage + i * 1024);  // rows kRowsPerInst * i ..: 1 KiB per instruction
-    dma16(kpool + off, dst);
-    dma16(vpool + off, dst + 32 * L::kRowBytes);
+    const uint32_t row_bytes = (uint32_t)(p_s0 * sizeof(T));
+    dma16(row_ptr(kpool + 8 * chunk, (uint32_t)keys[i], row_bytes), dst);
+    dma16(row_ptr(vpool + 8 * chunk, (uint32_t)keys[i], row_bytes), dst + 32 * L::kRowBytes);
   }
 }
 
@@ -97,6 +97,13 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
   const int seq = bid % a.batch;
   const int part = bid / a.batch;
 
+  // In a packed pass (qsl set) this kernel serves the one-query sequences;
+  // their query and output rows are where the pass packs them.
+  int row = seq;
+  if (a.qsl) {
+    row = a.qsl[seq];
+    if (a.qsl[seq + 1] - row != 1) return;
+  }
   const int ctx = a.ctx[seq];
   const int plen = a.part_len > 0 ? a.part_len : max(1, (ctx + a.num_parts - 1) / a.num_parts);
   const int kb = part * plen;
@@ -109,7 +116,7 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
 
   Frag qf[kSteps];
   {
-    const T* qrow = static_cast<const T*>(a.q) + (int64_t)seq * a.q_s0 + (int64_t)head * a.q_s1 + 8 * g;
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)row * a.q_s0 + (int64_t)head * a.q_s1 + 8 * g;
 #pragma unroll
     for (int j = 0; j < kSteps; ++j) {
       if (real_head) {
@@ -177,8 +184,7 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
         x[e] = (t0 + kappa(g, e) < c1) ? x[e] * sc : -INFINITY;
         mx = fmaxf(mx, x[e]);
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      mx = li_group_max(mx);
       const float mnew = fmaxf(m, mx);
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);
       float psum = 0.f;
@@ -237,13 +243,12 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
     li_wait_vm<0>();
   }
 
-  float lt = l + __shfl_xor(l, 16, 64);
-  lt = lt + __shfl_xor(lt, 32, 64);
+  const float lt = li_group_sum(l);
   if (!real_head) return;
   const float inv = 1.f / lt;
 
   if (nparts == 1) {
-    T* orow = static_cast<T*>(a.out) + (int64_t)seq * a.o_s0 + (int64_t)head * a.o_s1;
+    T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head * a.o_s1;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int chunk = 4 * g + r;

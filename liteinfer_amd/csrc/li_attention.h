@@ -38,6 +38,7 @@ struct AttnArgs {
   int block_q, block_kv;  // general-shape kernel tiles
   int num_qblocks;        // query blocks per sequence in the grid
   int max_query_len;      // most queries any sequence brings (prefill)
+  int single_query_elsewhere;  // prefill: one-query sequences are served by the decode kernel
 };
 
 // Largest head_dim the general-shape kernel serves.

@@ -78,6 +78,34 @@ __device__ __forceinline__ void li_wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
+// Max / sum over the four lanes n, n + 16, n + 32, n + 48 (the lane groups
+// that hold one MFMA column), every lane getting the result. Two permlane
+// swaps (gfx950) instead of LDS-crossbar shuffles: the rows of 16 lanes are
+// exchanged in registers, with no LDS round trip and no index arithmetic.
+__device__ __forceinline__ float li_group_max(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const uint32_t v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float li_group_sum(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const uint32_t v = __float_as_uint(y);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// 64-bit address of element `row * row_elems` of `base` in one multiply-add
+// (row and row stride both fit 32 bits).
+template <typename T>
+__device__ __forceinline__ const T* row_ptr(const T* base, uint32_t row, uint32_t row_bytes) {
+  return reinterpret_cast<const T*>(reinterpret_cast<uintptr_t>(base) + (uint64_t)row * row_bytes);
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(p);
 }

@@ -179,16 +179,29 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
   return rc;
 }
 
+extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,
+                                     int num_cus, size_t* workspace_bytes) {
+  clear_error();
+  if (int rc = check_common(LI_BF16, num_heads, num_kv_heads, head_dim, "li_paged_prefill_plan")) return rc;
+  if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_prefill_plan: negative extent");
+  if (num_cus <= 0) num_cus = device_cu_count();
+  int parts = 1, plen = 0;
+  decode_policy(batch, num_kv_heads, max_context, num_cus, kDefaultBlockKv, &parts, &plen);
+  if (workspace_bytes) *workspace_bytes = decode_workspace(batch, num_heads, head_dim, parts);
+  return LI_OK;
+}
+
 extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool,
                                 const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
-                                const int64_t* slot_table, int64_t slot_table_stride,
+                                const int64_t* slot_table, int64_t slot_table_stride, int max_context,
                                 const int32_t* context_lens, const int32_t* query_start_loc, int batch,
                                 int max_query_len, void* out, int64_t out_stride_tok, int64_t out_stride_head,
                                 int num_heads, int num_kv_heads, int head_dim, float scale, int block_q,
-                                int block_kv, int dtype, int flags, void* stream) {
+                                int block_kv, void* workspace, size_t workspace_bytes, int dtype, int flags,
+                                void* stream) {
   clear_error();
   if (int rc = check_common(dtype, num_heads, num_kv_heads, head_dim, "li_paged_prefill")) return rc;
-  if (batch < 0 || max_query_len < 0) return fail(LI_EINVAL, "li_paged_prefill: negative extent");
+  if (batch < 0 || max_query_len < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_prefill: negative extent");
   if (batch == 0 || max_query_len == 0) return LI_OK;
   if (!q || !key_pool || !value_pool || !slot_table || !context_lens || !query_start_loc || !out)
     return fail(LI_EINVAL, "li_paged_prefill: null pointer");
@@ -221,6 +234,31 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!(flags & LI_FLAG_FORCE_GENERIC) && prefill_mfma_applies(a, dtype)) {
+    // One-query sequences (decode rows beside chunks) would leave 127 of a
+    // prefill block's 128 rows idle and walk their whole context in one
+    // work-group; the decode kernel serves them instead, its key axis cut
+    // into partitions, and the prefill kernel skips them.
+    int parts = 1, plen = 0;
+    decode_policy(batch, num_kv_heads, max_context, device_cu_count(), kDefaultBlockKv, &parts, &plen);
+    const size_t need = decode_workspace(batch, num_heads, head_dim, parts);
+    if (need > 0 && (!workspace || workspace_bytes < need))
+      return fail(LI_EWORKSPACE, "li_paged_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+    AttnArgs d = a;
+    d.num_parts = parts;
+    d.part_len = plen;
+    d.block_q = 1;
+    d.num_qblocks = 1;
+    if (parts > 1) {
+      const size_t rows = (size_t)batch * num_heads * parts;
+      d.part_o = static_cast<float*>(workspace);
+      d.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * head_dim * sizeof(float)));
+    }
+    if (int rc = launch_decode_mfma(d, dtype, s)) return rc;
+    if (parts > 1) {
+      if (int rc = launch_combine(d, dtype, s)) return rc;
+    }
+    if (max_query_len <= 1) return LI_OK;
+    a.single_query_elsewhere = 1;
     return launch_prefill_mfma(a, dtype, s);
   }
   a.block_q = block_q > 0 ? block_q : 16;

@@ -49,7 +49,7 @@ constexpr int kStageKeys = 64;
 // instructions i = w * kInsts / 4 + ... (K and V).
 template <typename T, int D>
 __device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ kpool, const T* __restrict__ vpool,
-                                            const int* __restrict__ sl, int64_t p_s0, int t, int lane, int w) {
+                                            const int* __restrict__ sl, uint32_t row_bytes, int t, int lane, int w) {
   using L = TileLayout<D>;
   constexpr int kPerWave = L::kInsts / kWaves;
   const int rr = lane / L::kCh, nn = lane % L::kCh;
@@ -60,12 +60,11 @@ __device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ k
     for (int ii = 0; ii < kPerWave; ++ii) {
       const int i = w * kPerWave + ii;
       const int key = rr * L::kInsts + i;
-      const int slot = sl[t + 32 * half + key];
+      const uint32_t slot = (uint32_t)sl[t + 32 * half + key];
       const int chunk = nn ^ (key % L::kCh);
-      const int64_t off = (int64_t)slot * p_s0 + 8 * chunk;
       const uint32_t dst = lds_addr(tile + i * 1024);
-      dma16(kpool + off, dst);
-      dma16(vpool + off, dst + 32 * L::kRowBytes);
+      dma16(row_ptr(kpool + 8 * chunk, slot, row_bytes), dst);
+      dma16(row_ptr(vpool + 8 * chunk, slot, row_bytes), dst + 32 * L::kRowBytes);
     }
   }
 }
@@ -97,6 +96,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int bq = a.block_q;  // query tokens per block = kRows / groups
   const int q0 = qblock * bq;
   if (q0 >= nq) return;
+  if (nq == 1 && a.single_query_elsewhere) return;  // the decode kernel serves it
   const int q1 = min(q0 + bq, nq);
   const int ctx = a.ctx[seq];
   const int pos0 = ctx - nq;   // position of the sequence's first query
@@ -129,10 +129,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Last key each row sees: its own position (padding rows: the block's last key).
   const int lim[2] = {min(pos[0], kend - 1), min(pos[1], kend - 1)};
+  // Below the block's first query position every row sees every key.
+  const int lim_lo = min(pos0 + q0, kend - 1);
 
   const T* kpool = static_cast<const T*>(a.kp) + (int64_t)kvh * a.p_s1;
   const T* vpool = static_cast<const T*>(a.vp) + (int64_t)kvh * a.p_s1;
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
+  const uint32_t row_bytes = (uint32_t)(a.p_s0 * sizeof(T));
   const float sc = a.scale * kLog2eMfma;
 
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
@@ -172,14 +175,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         x[r] = s[nb][0][r];
         x[4 + r] = s[nb][1][r];
       }
+      if (t0 + 31 > lim_lo) {  // the tile reaches past some row's last key
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (t0 + kappa(g, e) <= lim[nb]) ? x[e] : -INFINITY;
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[e] = (t0 + kappa(g, e) <= lim[nb]) ? x[e] : -INFINITY;
-        mx = fmaxf(mx, x[e]);
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x[e]);
+      mx = li_group_max(mx);
       mx *= sc;
       // Lazy rescale: the running maximum only moves when a tile beats it by
       // more than kLazyRescale (log2 units), so most tiles leave the
@@ -247,9 +250,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // Two stages: the next 64 keys land in one while the other is folded.
     // Past the chunk the look-ahead re-reads a real stage (cache hits), so
     // every wave has the same loads in flight at every wait.
-    issue_stage<T, D>(stages[0], kpool, vpool, sl, a.p_s0, 0, lane, w);
+    issue_stage<T, D>(stages[0], kpool, vpool, sl, row_bytes, 0, lane, w);
     for (int ti = 0; ti < ntiles; ++ti) {
-      issue_stage<T, D>(stages[(ti + 1) & 1], kpool, vpool, sl, a.p_s0, min(kStageKeys * (ti + 1), kSlotChunk),
+      issue_stage<T, D>(stages[(ti + 1) & 1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kSlotChunk),
                         lane, w);
       li_wait_vm<kDmaPerStage>();
       __syncthreads();
@@ -264,8 +267,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    float lt = l[nb] + __shfl_xor(l[nb], 16, 64);
-    lt = lt + __shfl_xor(lt, 32, 64);
+    const float lt = li_group_sum(l[nb]);
     if (!real[nb]) continue;
     const float inv = 1.f / lt;
     T* orow = static_cast<T*>(a.out) + (int64_t)tok[nb] * a.o_s0 + (int64_t)head[nb] * a.o_s1;

@@ -13,7 +13,9 @@ C-ABI library in ``csrc/`` on torch's current stream:
   writes fp32 partials and a log-sum-exp per partition, and a second launch
   weighs them together.
 * `paged_prefill` — packed queries, causal within each sequence's chunk,
-  over the prefix the pool already holds.
+  over the prefix the pool already holds. Its one-query sequences (decode
+  rows beside chunks) run on the decode kernel, partitioned, in the same
+  call.
 
 bf16/fp16 pools with head_dim 64 or 128 and up to 16 query heads per KV head
 run on the MFMA kernels; every other shape (fp32 above all) on a
@@ -304,16 +306,25 @@ def paged_prefill(
     if query_start_loc.shape[0] != batch + 1:
         raise ValueError(f"query_start_loc has {query_start_loc.shape[0]} entries for {batch} sequences")
     num_kv_heads = key_pool.shape[1]
+    max_context = slot_table.shape[1]
 
-    out = torch.empty_like(query)
     lib = _native.load()
+    need = _native.ctypes.c_size_t()
+    status = lib.li_paged_prefill_plan(
+        batch, num_heads, num_kv_heads, head_dim, max_context, _compute_unit_count(device.index or 0),
+        _native.ctypes.byref(need),
+    )
+    _native.check(status, "paged_prefill")
+    out = torch.empty_like(query)
+    workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
     status = lib.li_paged_prefill(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
-        slot_table.data_ptr(), slot_table.stride(0),
+        slot_table.data_ptr(), slot_table.stride(0), max_context,
         context_lens.data_ptr(), query_start_loc.data_ptr(), batch, int(max_query_len),
         out.data_ptr(), out.stride(0), out.stride(1),
         num_heads, num_kv_heads, head_dim, float(scaling), block_q, block_kv,
+        workspace.data_ptr() if workspace is not None else None, need.value,
         _native.dtype_code(query.dtype), _flags(kernel), _native.stream_handle(device),
     )
     _native.check(status, "paged_prefill")
