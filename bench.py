@@ -175,6 +175,9 @@ def main() -> int:
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true", help="skip configs 3 and 4")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="first run three 1 GiB device-to-device copies (a reference kernel of known "
+                             "size for rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
     args = parser.parse_args()
 
     if args.gpus != 1:
@@ -187,6 +190,13 @@ def main() -> int:
         return 2
     _native.load()
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     step = decode_step("c2", seed=args.seed)
     geo = step.geometry

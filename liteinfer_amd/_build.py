@@ -34,6 +34,7 @@ DEVICE_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-honor-nans",
     "-Wall",
     "-Wno-unused-function",
 ]

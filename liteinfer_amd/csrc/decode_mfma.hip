@@ -72,88 +72,51 @@ __device__ __forceinline__ void issue_tile(char* stage, const T* __restrict__ kp
   }
 }
 
-template <typename T, int D, int kStages>
-__global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
+// LDS of one decode wave: the staged slots of a chunk and two tile stages.
+template <int D>
+struct DecodeLds {
+  int sl[kSlotChunk + 64];
+  char stage[2][TileLayout<D>::kTileBytes];
+};
+
+// Online-softmax state of one wave: lane (n, g) holds head n's running max
+// and (partial) denominator, and dims {8(4g+r) + i} of its accumulator.
+struct DecodeState {
+  float m, l;
+  floatx4_t acc[8];
+};
+
+// Folds keys [kb, ke) of sequence `seq`'s context for KV head `kvh` into `st`.
+// qf holds this lane's head's query (zeros for heads past the group).
+template <typename T, int D>
+__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, const typename Mfma<T>::Frag* qf,
+                                          int seq, int kvh, int kb, int ke, DecodeState& st) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
   using L = TileLayout<D>;
   constexpr int kSteps = D / 32;
   constexpr int kChunks = D / 8;
-  __shared__ __attribute__((aligned(16))) int sl[kSlotChunk + 64];
-  // Two stages as separate LDS objects, so the compiler can tell a read of
-  // one from the direct-to-LDS loads still landing in the other.
-  __shared__ __attribute__((aligned(1024))) char stage0[L::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char stage1[L::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char stage2[kStages == 3 ? L::kTileBytes : 16];
-
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
-  // Partition-major order: every sequence's first partition is dispatched
-  // before any second one, so the grid's empty tail (partitions past a short
-  // context) comes last and exits at once.
-  int bid = blockIdx.x;
-  const int kvh = bid % a.num_kv_heads;
-  bid /= a.num_kv_heads;
-  const int seq = bid % a.batch;
-  const int part = bid / a.batch;
-
-  // In a packed pass (qsl set) this kernel serves the one-query sequences;
-  // their query and output rows are where the pass packs them.
-  int row = seq;
-  if (a.qsl) {
-    row = a.qsl[seq];
-    if (a.qsl[seq + 1] - row != 1) return;
-  }
-  const int ctx = a.ctx[seq];
-  const int plen = a.part_len > 0 ? a.part_len : max(1, (ctx + a.num_parts - 1) / a.num_parts);
-  const int kb = part * plen;
-  if (kb >= ctx) return;
-  const int ke = min(kb + plen, ctx);
-  const int nparts = (ctx + plen - 1) / plen;
-
-  const bool real_head = n < a.groups;
-  const int head = kvh * a.groups + n;
-
-  Frag qf[kSteps];
-  {
-    const T* qrow = static_cast<const T*>(a.q) + (int64_t)row * a.q_s0 + (int64_t)head * a.q_s1 + 8 * g;
-#pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
-      if (real_head) {
-        qf[j] = *reinterpret_cast<const Frag*>(qrow + 32 * j);
-      } else {
-        qf[j] = Frag{};
-      }
-    }
-  }
-
   const T* kpool = static_cast<const T*>(a.kp) + (int64_t)kvh * a.p_s1;
   const T* vpool = static_cast<const T*>(a.vp) + (int64_t)kvh * a.p_s1;
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
   const float sc = a.scale * kLog2eMfma;
 
-  float m = -INFINITY, l = 0.f;
-  floatx4_t acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-
   for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
     const int c1 = min(c0 + kSlotChunk, ke);
-    const int len = c1 - c0;
-    const int ntiles = (len + 31) / 32;
+    const int ntiles = (c1 - c0 + 31) / 32;
     // Stage this chunk's slots (int32: a pool holds fewer than 2^31 slots),
-    // plus two tiles past its end. Entries past the chunk repeat its last
-    // slot, so the loads of a partial tile read real rows; their scores are
-    // masked.
-    __syncthreads();
+    // plus a tile past its end. Entries past the chunk repeat its last slot,
+    // so the loads of a partial or look-ahead tile read real rows; their
+    // scores are masked.
     {
       int vals[kSlotChunk / 64 + 1];
 #pragma unroll
       for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
 #pragma unroll
-      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) sl[lane + 64 * k] = vals[k];
+      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
     }
-    __syncthreads();
 
     // Folds the tile in `stage` whose first key is t0.
     auto fold = [&](const char* stage, int t0) {
@@ -178,23 +141,32 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
         x[r] = s0[r];
         x[4 + r] = s1[r];
       }
+      if (t0 + 32 > c1) {  // a partial tile: mask the keys past the chunk
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = (t0 + kappa(g, e) < c1) ? x[e] : -INFINITY;
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        x[e] = (t0 + kappa(g, e) < c1) ? x[e] * sc : -INFINITY;
-        mx = fmaxf(mx, x[e]);
-      }
-      mx = li_group_max(mx);
-      const float mnew = fmaxf(m, mx);
-      const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x[e]);
+      mx = li_group_max(mx) * sc;
+      // Lazy rescale (see kLazyRescale).
+      const float mnew = (mx > st.m + kLazyRescale) ? mx : st.m;
+      const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
       float psum = 0.f;
       float p[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        p[e] = __builtin_amdgcn_exp2f(x[e] - mnew);
+        p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
         psum += p[e];
       }
-      l = l * alpha + psum;
+      st.l = st.l * alpha + psum;
+      if (__any(mnew != st.m)) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) st.acc[i][r] *= alpha;
+      }
+      st.m = mnew;
       u32x4_t pw;
 #pragma unroll
       for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
@@ -208,60 +180,69 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
           const uint32_t lo = vr[2 * u][w], hi = vr[2 * u + 1][w];
           va[u] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[i][r] *= alpha;
-        acc[i] = M::mma(__builtin_bit_cast(Frag, va), pf, acc[i]);
+        st.acc[i] = M::mma(__builtin_bit_cast(Frag, va), pf, st.acc[i]);
       }
-      m = mnew;
     };
 
-    // kStages stages: while one tile is folded the next kStages - 1 tiles'
-    // loads land in the others. Past the chunk the look-ahead re-reads a real
-    // tile (cache hits), so the loads in flight are the same every step and
-    // no load sits under a branch.
-    constexpr int kInFlight = 2 * L::kInsts * (kStages - 1);
-    issue_tile<T, D>(stage0, kpool, vpool, sl, a.p_s0, 0, lane);
-    if constexpr (kStages == 3) issue_tile<T, D>(stage1, kpool, vpool, sl, a.p_s0, min(32, kSlotChunk), lane);
+    // Two stages: while one tile is folded the next tile's loads land in the
+    // other. Past the chunk the look-ahead re-reads a real tile (cache hits),
+    // so the loads in flight are the same every step and no load sits under
+    // a branch.
+    constexpr int kInFlight = 2 * L::kInsts;
+    issue_tile<T, D>(lds.stage[0], kpool, vpool, lds.sl, a.p_s0, 0, lane);
     for (int ti = 0;;) {
-      issue_tile<T, D>(kStages == 3 ? stage2 : stage1, kpool, vpool, sl, a.p_s0,
-                       min(32 * (ti + kStages - 1), kSlotChunk), lane);
+      issue_tile<T, D>(lds.stage[1], kpool, vpool, lds.sl, a.p_s0, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
-      fold(stage0, c0 + 32 * ti);
+      fold(lds.stage[0], c0 + 32 * ti);
       if (++ti >= ntiles) break;
-      issue_tile<T, D>(stage0, kpool, vpool, sl, a.p_s0, min(32 * (ti + kStages - 1), kSlotChunk), lane);
+      issue_tile<T, D>(lds.stage[0], kpool, vpool, lds.sl, a.p_s0, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
-      fold(stage1, c0 + 32 * ti);
+      fold(lds.stage[1], c0 + 32 * ti);
       if (++ti >= ntiles) break;
-      if constexpr (kStages == 3) {
-        issue_tile<T, D>(stage1, kpool, vpool, sl, a.p_s0, min(32 * (ti + kStages - 1), kSlotChunk), lane);
-        li_wait_vm<kInFlight>();
-        fold(stage2, c0 + 32 * ti);
-        if (++ti >= ntiles) break;
-      }
     }
     // Drain the look-ahead loads before the slots (and stages) are reused.
     li_wait_vm<0>();
   }
+}
 
-  const float lt = li_group_sum(l);
-  if (!real_head) return;
+// Loads the query fragments of KV head `kvh`'s group for the query at `row`.
+template <typename T, int D>
+__device__ __forceinline__ void load_query(const AttnArgs& a, int row, int kvh, typename Mfma<T>::Frag* qf) {
+  using Frag = typename Mfma<T>::Frag;
+  const int lane = threadIdx.x;
+  const int n = lane & 15, g = lane >> 4;
+  const T* qrow = static_cast<const T*>(a.q) + (int64_t)row * a.q_s0 + (int64_t)(kvh * a.groups + n) * a.q_s1 + 8 * g;
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) qf[j] = (n < a.groups) ? *reinterpret_cast<const Frag*>(qrow + 32 * j) : Frag{};
+}
+
+// Writes a finished softmax: the normalised output row of each head of the
+// group to `out` (dtype T), or, for a piece of a context, the fp32 normalised
+// partial of head n to po + n * p_head_stride * D and its log2-domain LSE to
+// plse[n * p_head_stride].
+template <typename T, int D>
+__device__ __forceinline__ void store_state(const DecodeState& st, T* orow_head0, int64_t o_s1, float* po,
+                                            float* plse, int64_t p_head_stride, int groups) {
+  constexpr int kChunks = D / 8;
+  const int lane = threadIdx.x;
+  const int n = lane & 15, g = lane >> 4;
+  const float lt = li_group_sum(st.l);
+  if (n >= groups) return;
   const float inv = 1.f / lt;
-
-  if (nparts == 1) {
-    T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head * a.o_s1;
+  if (orow_head0) {
+    T* orow = orow_head0 + (int64_t)n * o_s1;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int chunk = 4 * g + r;
       if (chunk < kChunks) {
         u32x4_t w;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = li_pack2<T>(acc[2 * u][r] * inv, acc[2 * u + 1][r] * inv);
+        for (int u = 0; u < 4; ++u) w[u] = li_pack2<T>(st.acc[2 * u][r] * inv, st.acc[2 * u + 1][r] * inv);
         *reinterpret_cast<u32x4_t*>(orow + 8 * chunk) = w;
       }
     }
   } else {
-    const int64_t base = ((int64_t)seq * a.num_heads + head) * a.num_parts + part;
-    float* po = a.part_o + base * D;
+    float* prow = po + (int64_t)n * p_head_stride * D;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int chunk = 4 * g + r;
@@ -269,14 +250,248 @@ __global__ __launch_bounds__(64) void decode_mfma(AttnArgs a) {
         floatx4_t lo4, hi4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          lo4[i] = acc[i][r] * inv;
-          hi4[i] = acc[4 + i][r] * inv;
+          lo4[i] = st.acc[i][r] * inv;
+          hi4[i] = st.acc[4 + i][r] * inv;
         }
-        *reinterpret_cast<floatx4_t*>(po + 8 * chunk) = lo4;
-        *reinterpret_cast<floatx4_t*>(po + 8 * chunk + 4) = hi4;
+        *reinterpret_cast<floatx4_t*>(prow + 8 * chunk) = lo4;
+        *reinterpret_cast<floatx4_t*>(prow + 8 * chunk + 4) = hi4;
       }
     }
-    if (g == 0) a.part_lse[base] = m + log2f(lt);
+    if (g == 0) plse[(int64_t)n * p_head_stride] = st.m + log2f(lt);
+  }
+}
+
+__device__ __forceinline__ void reset_state(DecodeState& st) {
+  st.m = -INFINITY;
+  st.l = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) st.acc[i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+}
+
+// Query row of sequence `seq`, or -1 when the decode kernel does not serve
+// it (in a packed pass, sequences with more than one query).
+__device__ __forceinline__ int decode_row(const AttnArgs& a, int seq) {
+  if (!a.qsl) return seq;
+  const int f = a.qsl[seq];
+  return (a.qsl[seq + 1] - f == 1) ? f : -1;
+}
+
+// Keys of sequence `seq` the decode kernel folds, per KV head.
+__device__ __forceinline__ int decode_keys(const AttnArgs& a, int seq) {
+  return decode_row(a, seq) < 0 ? 0 : max(a.ctx[seq], 0);
+}
+
+// ---------------------------------------------------------------------------
+// Partitioned decode: one wave per (sequence, KV head, partition). Serves a
+// pinned split count (the reference's equal-slice rule: partition p of a
+// context of c keys is [p * cdiv(c, S), ...)).
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__global__ __launch_bounds__(64) void decode_partitioned(AttnArgs a) {
+  using Frag = typename Mfma<T>::Frag;
+  __shared__ __attribute__((aligned(1024))) DecodeLds<D> lds;
+  // Partition-major order: every sequence's first partition is dispatched
+  // before any second one, so the grid's empty tail comes last.
+  int bid = blockIdx.x;
+  const int kvh = bid % a.num_kv_heads;
+  bid /= a.num_kv_heads;
+  const int seq = bid % a.batch;
+  const int part = bid / a.batch;
+  const int row = decode_row(a, seq);
+  if (row < 0) return;
+  const int ctx = a.ctx[seq];
+  const int plen = a.part_len > 0 ? a.part_len : max(1, (ctx + a.num_parts - 1) / a.num_parts);
+  const int kb = part * plen;
+  if (kb >= ctx) return;
+  const int ke = min(kb + plen, ctx);
+  const int nparts = (ctx + plen - 1) / plen;
+
+  Frag qf[D / 32];
+  load_query<T, D>(a, row, kvh, qf);
+  DecodeState st;
+  reset_state(st);
+  fold_keys<T, D>(a, lds, qf, seq, kvh, kb, ke, st);
+  const int head0 = kvh * a.groups;
+  if (nparts == 1) {
+    store_state<T, D>(st, static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head0 * a.o_s1, a.o_s1,
+                      nullptr, nullptr, 0, a.groups);
+  } else {
+    // partials [batch, num_heads, num_parts, D]: head h's row is (seq * Hq + h) * P + part
+    const int64_t base = ((int64_t)seq * a.num_heads + head0) * a.num_parts + part;
+    store_state<T, D>(st, nullptr, 0, a.part_o + base * D, a.part_lse + base, a.num_parts, a.groups);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Balanced decode: a fixed grid of W waves splits the flattened key space
+// (sequence-major, then KV head, then key) into equal shares of whole
+// 32-key tiles. A wave walks the (sequence, KV head) segments its share
+// covers, carrying nothing between them; a segment that is a whole context
+// is written as output, a piece of one as an fp32 partial in one of the
+// wave's two partial slots (0: the segment holding the wave's first key,
+// 1: its last segment). Every wave does the same work whatever the spread of
+// context lengths, and there are no empty work-groups. W comes from the host
+// (a multiple of the CU count), the shares from device data, so a captured
+// graph replays for any contexts.
+// ---------------------------------------------------------------------------
+
+// Sum of v over the wave, exact for integers.
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const int lo = __shfl_xor((int)(v & 0xffffffff), off, 64);
+    const int hi = __shfl_xor((int)(v >> 32), off, 64);
+    v += ((int64_t)hi << 32) | (uint32_t)lo;
+  }
+  return v;
+}
+
+// Total keys (all sequences, all KV heads) and the share of each wave.
+__device__ __forceinline__ void balanced_share(const AttnArgs& a, int64_t& total, int64_t& share) {
+  const int lane = threadIdx.x;
+  int64_t t = 0;
+  for (int s0 = 0; s0 < a.batch; s0 += 64) {
+    const int s = s0 + lane;
+    t += s < a.batch ? (int64_t)decode_keys(a, s) : 0;
+  }
+  total = wave_sum_i64(t) * a.num_kv_heads;
+  const int64_t waves = a.num_parts;
+  share = ((total + waves - 1) / waves + 31) / 32 * 32;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
+  using Frag = typename Mfma<T>::Frag;
+  __shared__ __attribute__((aligned(1024))) DecodeLds<D> lds;
+  const int lane = threadIdx.x;
+  const int w = blockIdx.x;
+  int64_t total, share;
+  balanced_share(a, total, share);
+  int64_t pos = (int64_t)w * share;
+  if (pos >= total) return;
+  const int64_t end = min(pos + share, total);
+
+  // Find the sequence holding flattened key `pos`: scan 64 sequences at a time.
+  int seq = 0;
+  int64_t before = 0;  // flattened keys of the sequences before `seq`
+  for (int s0 = 0; s0 < a.batch; s0 += 64) {
+    const int s = s0 + lane;
+    const int64_t c = s < a.batch ? (int64_t)decode_keys(a, s) * a.num_kv_heads : 0;
+    int64_t incl = c;  // inclusive prefix within this group of 64
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int lo = __shfl_up((int)(incl & 0xffffffff), off, 64);
+      const int hi = __shfl_up((int)(incl >> 32), off, 64);
+      if (lane >= off) incl += ((int64_t)hi << 32) | (uint32_t)lo;
+    }
+    const uint64_t hit = __ballot(before + incl > pos);
+    if (hit) {
+      const int first = __ffsll((long long)hit) - 1;
+      const int64_t excl = __shfl(incl - c, first, 64);
+      seq = s0 + first;
+      before += excl;
+      break;
+    }
+    before += __shfl(incl, 63, 64);
+  }
+
+  int ctx = decode_keys(a, seq);
+  int64_t local = pos - before;
+  int kvh = (int)(local / ctx);
+  int key0 = (int)(local - (int64_t)kvh * ctx);
+  const int G = a.groups;
+  float* part_o = a.part_o + (int64_t)w * 2 * G * a.head_dim;
+  float* part_lse = a.part_lse + (int64_t)w * 2 * G;
+  bool first_segment = true;
+  while (pos < end) {
+    const int take = (int)min((int64_t)(ctx - key0), end - pos);
+    const int row = decode_row(a, seq);
+    Frag qf[D / 32];
+    load_query<T, D>(a, row, kvh, qf);
+    DecodeState st;
+    reset_state(st);
+    fold_keys<T, D>(a, lds, qf, seq, kvh, key0, key0 + take, st);
+    if (key0 == 0 && take == ctx) {
+      store_state<T, D>(st, static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)kvh * G * a.o_s1, a.o_s1,
+                        nullptr, nullptr, 0, G);
+    } else {
+      const int slot = first_segment ? 0 : 1;
+      store_state<T, D>(st, nullptr, 0, part_o + (int64_t)slot * G * a.head_dim, part_lse + slot * G, 1, G);
+    }
+    pos += take;
+    first_segment = false;
+    key0 = 0;
+    if (++kvh == a.num_kv_heads) {
+      kvh = 0;
+      do {
+        ++seq;
+      } while (pos < end && seq < a.batch && decode_keys(a, seq) == 0);
+      if (seq >= a.batch) break;
+      ctx = decode_keys(a, seq);
+    }
+  }
+}
+
+// Folds the pieces of each (sequence, head) the balanced kernel split across
+// waves: w_p = 2^(lse_p - max lse), out = sum w_p o_p / sum w_p
+// (paged_kernels.py:574-629, in the log2 domain). One wave per (head,
+// sequence); a context no wave boundary cut was written directly.
+template <typename T>
+__global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
+  constexpr int kMaxC = kGenericMaxHeadDim / 64;
+  const int lane = threadIdx.x;
+  const int head = blockIdx.x % a.num_heads;
+  const int seq = blockIdx.x / a.num_heads;
+  const int ctx = decode_keys(a, seq);
+  if (ctx == 0) return;
+  int64_t total, share;
+  balanced_share(a, total, share);
+  // Flattened offset of this (sequence, KV head).
+  int64_t before = 0;
+  for (int s0 = 0; s0 < seq; s0 += 64) {
+    const int s = s0 + lane;
+    before += (s < seq) ? (int64_t)decode_keys(a, s) : 0;
+  }
+  const int G = a.groups;
+  const int kvh = head / G, h = head % G;
+  const int64_t off = wave_sum_i64(before) * a.num_kv_heads + (int64_t)kvh * ctx;
+  const int64_t w0 = off / share, w1 = (off + ctx - 1) / share;
+  if (w0 == w1) return;
+  const int D = a.head_dim;
+  const int n = (int)(w1 - w0 + 1);
+
+  // Weights: lane j holds piece j, j + 64, ...
+  float mx = -INFINITY;
+  for (int j = lane; j < n; j += 64) {
+    const int64_t w = w0 + j;
+    const int slot = (w * share >= off) ? 0 : 1;
+    mx = fmaxf(mx, a.part_lse[(w * 2 + slot) * G + h]);
+  }
+  mx = li_wave_max(mx);
+  float acc[kMaxC];
+#pragma unroll
+  for (int c = 0; c < kMaxC; ++c) acc[c] = 0.f;
+  float wsum = 0.f;
+  for (int j = 0; j < n; ++j) {
+    const int64_t w = w0 + j;
+    const int slot = (w * share >= off) ? 0 : 1;
+    const int64_t r = (w * 2 + slot) * G + h;
+    const float wt = exp2f(a.part_lse[r] - mx);
+    wsum += wt;
+    const float* po = a.part_o + r * D;
+#pragma unroll
+    for (int c = 0; c < kMaxC; ++c) {
+      const int d = lane + 64 * c;
+      if (d < D) acc[c] = fmaf(wt, po[d], acc[c]);
+    }
+  }
+  const float inv = 1.f / wsum;
+  const int row = decode_row(a, seq);
+  T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head * a.o_s1;
+#pragma unroll
+  for (int c = 0; c < kMaxC; ++c) {
+    const int d = lane + 64 * c;
+    if (d < D) orow[d] = li_from_float<T>(acc[c] * inv);
   }
 }
 
@@ -295,26 +510,32 @@ bool decode_mfma_applies(const AttnArgs& a, int dtype) {
 }
 
 int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
-  const int64_t blocks = (int64_t)a.batch * a.num_kv_heads * a.num_parts;
+  const bool balanced = a.part_len < 0;
+  const int64_t blocks = balanced ? a.num_parts : (int64_t)a.batch * a.num_kv_heads * a.num_parts;
   if (blocks == 0) return LI_OK;
   if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "decode grid of %lld blocks is too large", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(64);
-  static const int stages = [] {
-    const char* v = std::getenv("LI_DECODE_STAGES");
-    return (v && v[0] == '3') ? 3 : 2;
-  }();
+#define LI_DECODE_LAUNCH(T, D)                                                   \
+  do {                                                                           \
+    if (balanced) hipLaunchKernelGGL((decode_balanced<T, D>), grid, block, 0, s, a); \
+    else hipLaunchKernelGGL((decode_partitioned<T, D>), grid, block, 0, s, a);       \
+  } while (0)
   if (dtype == LI_BF16) {
-    if (a.head_dim == 128) {
-      if (stages == 3) hipLaunchKernelGGL((decode_mfma<li_bf16, 128, 3>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((decode_mfma<li_bf16, 128, 2>), grid, block, 0, s, a);
-    } else {
-      hipLaunchKernelGGL((decode_mfma<li_bf16, 64, 2>), grid, block, 0, s, a);
-    }
+    if (a.head_dim == 128) LI_DECODE_LAUNCH(li_bf16, 128);
+    else LI_DECODE_LAUNCH(li_bf16, 64);
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((decode_mfma<li_f16, 128, 2>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((decode_mfma<li_f16, 64, 2>), grid, block, 0, s, a);
+    if (a.head_dim == 128) LI_DECODE_LAUNCH(li_f16, 128);
+    else LI_DECODE_LAUNCH(li_f16, 64);
   }
-  return check_launch("decode_mfma");
+#undef LI_DECODE_LAUNCH
+  if (int rc = check_launch("decode_mfma")) return rc;
+  if (balanced) {
+    const int64_t cblocks = (int64_t)a.batch * a.num_heads;
+    if (dtype == LI_BF16) hipLaunchKernelGGL(combine_balanced<li_bf16>, dim3((unsigned)cblocks), dim3(64), 0, s, a);
+    else hipLaunchKernelGGL(combine_balanced<li_f16>, dim3((unsigned)cblocks), dim3(64), 0, s, a);
+    return check_launch("combine_balanced");
+  }
+  return LI_OK;
 }
 
 }  // namespace li

@@ -66,6 +66,31 @@ size_t decode_workspace(int batch, int num_heads, int head_dim, int parts) {
   return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
 }
 
+// Balanced decode (the MFMA kernel's automatic mode): a fixed grid of waves,
+// kBalancedWavesPerCu per CU (the LDS of four waves fills a CU), splits the
+// flattened key space into equal shares; each wave keeps up to two fp32
+// partials of `groups` heads.
+constexpr int kBalancedWavesPerCu = 4;
+
+int balanced_waves(int num_cus) {
+  static const int per_cu = env_int("LI_DECODE_BALANCED_WAVES_PER_CU", kBalancedWavesPerCu);
+  return std::max(1, num_cus) * per_cu;
+}
+
+size_t balanced_workspace(int waves, int groups, int head_dim) {
+  const size_t rows = (size_t)waves * 2 * groups;
+  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+}
+
+// Points a balanced launch's partial buffers into `workspace`.
+void set_balanced(AttnArgs& d, int waves, void* workspace) {
+  d.num_parts = waves;
+  d.part_len = -1;
+  const size_t rows = (size_t)waves * 2 * d.groups;
+  d.part_o = static_cast<float*>(workspace);
+  d.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * d.head_dim * sizeof(float)));
+}
+
 int check_common(int dtype, int num_heads, int num_kv_heads, int head_dim, const char* who) {
   if (dtype_size(dtype) == 0) return fail(LI_EINVAL, "%s: unknown dtype %d", who, dtype);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -108,7 +133,13 @@ extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, 
   }
   if (num_partitions) *num_partitions = parts;
   if (partition_len) *partition_len = plen;
-  if (workspace_bytes) *workspace_bytes = decode_workspace(batch, num_heads, head_dim, parts);
+  size_t need = decode_workspace(batch, num_heads, head_dim, parts);
+  if (num_splits == 0) {
+    // The MFMA kernel's automatic mode is the balanced split; size for either.
+    if (num_cus <= 0) num_cus = device_cu_count();
+    need = std::max(need, balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim));
+  }
+  if (workspace_bytes) *workspace_bytes = need;
   return LI_OK;
 }
 
@@ -168,12 +199,18 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
   }
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  int rc;
-  if (!(flags & LI_FLAG_FORCE_GENERIC) && decode_mfma_applies(a, dtype)) {
-    rc = launch_decode_mfma(a, dtype, s);
-  } else {
-    rc = launch_attend_generic(a, dtype, s);
+  const bool mfma = !(flags & LI_FLAG_FORCE_GENERIC) && decode_mfma_applies(a, dtype);
+  if (mfma && num_splits == 0) {
+    // Automatic mode on the MFMA kernel: the balanced split (it launches its
+    // own combine).
+    const int waves = balanced_waves(device_cu_count());
+    if (balanced_workspace(waves, a.groups, head_dim) > workspace_bytes || !workspace)
+      return fail(LI_EWORKSPACE, "li_paged_decode: workspace of %zu bytes given, %zu needed", workspace_bytes,
+                  balanced_workspace(waves, a.groups, head_dim));
+    set_balanced(a, waves, workspace);
+    return launch_decode_mfma(a, dtype, s);
   }
+  int rc = mfma ? launch_decode_mfma(a, dtype, s) : launch_attend_generic(a, dtype, s);
   if (rc) return rc;
   if (parts > 1) rc = launch_combine(a, dtype, s);
   return rc;
@@ -185,9 +222,7 @@ extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
   if (int rc = check_common(LI_BF16, num_heads, num_kv_heads, head_dim, "li_paged_prefill_plan")) return rc;
   if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_prefill_plan: negative extent");
   if (num_cus <= 0) num_cus = device_cu_count();
-  int parts = 1, plen = 0;
-  decode_policy(batch, num_kv_heads, max_context, num_cus, kDefaultBlockKv, &parts, &plen);
-  if (workspace_bytes) *workspace_bytes = decode_workspace(batch, num_heads, head_dim, parts);
+  if (workspace_bytes) *workspace_bytes = balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim);
   return LI_OK;
 }
 
@@ -238,25 +273,15 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
     // prefill block's 128 rows idle and walk their whole context in one
     // work-group; the decode kernel serves them instead, its key axis cut
     // into partitions, and the prefill kernel skips them.
-    int parts = 1, plen = 0;
-    decode_policy(batch, num_kv_heads, max_context, device_cu_count(), kDefaultBlockKv, &parts, &plen);
-    const size_t need = decode_workspace(batch, num_heads, head_dim, parts);
-    if (need > 0 && (!workspace || workspace_bytes < need))
+    const int waves = balanced_waves(device_cu_count());
+    const size_t need = balanced_workspace(waves, a.groups, head_dim);
+    if (!workspace || workspace_bytes < need)
       return fail(LI_EWORKSPACE, "li_paged_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
     AttnArgs d = a;
-    d.num_parts = parts;
-    d.part_len = plen;
     d.block_q = 1;
     d.num_qblocks = 1;
-    if (parts > 1) {
-      const size_t rows = (size_t)batch * num_heads * parts;
-      d.part_o = static_cast<float*>(workspace);
-      d.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * head_dim * sizeof(float)));
-    }
+    set_balanced(d, waves, workspace);
     if (int rc = launch_decode_mfma(d, dtype, s)) return rc;
-    if (parts > 1) {
-      if (int rc = launch_combine(d, dtype, s)) return rc;
-    }
     if (max_query_len <= 1) return LI_OK;
     a.single_query_elsewhere = 1;
     return launch_prefill_mfma(a, dtype, s);
