@@ -405,6 +405,13 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
   bool first_segment = true;
   while (pos < end) {
     const int take = (int)min((int64_t)(ctx - key0), end - pos);
+    if (key0 == 0 && lane == 0) {
+      // This wave holds the context's first key: record which waves hold its
+      // pieces, and which of this wave's slots the first one is in.
+      const int64_t off = before + (int64_t)kvh * ctx;
+      a.pieces[(int64_t)seq * a.num_kv_heads + kvh] =
+          int4{w, (int)((off + ctx - 1) / share), first_segment ? 0 : 1, 0};
+    }
     const int row = decode_row(a, seq);
     Frag qf[D / 32];
     load_query<T, D>(a, row, kvh, qf);
@@ -423,9 +430,9 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
     key0 = 0;
     if (++kvh == a.num_kv_heads) {
       kvh = 0;
-      do {
-        ++seq;
-      } while (pos < end && seq < a.batch && decode_keys(a, seq) == 0);
+      before += (int64_t)ctx * a.num_kv_heads;
+      ++seq;
+      while (pos < end && seq < a.batch && decode_keys(a, seq) == 0) ++seq;
       if (seq >= a.batch) break;
       ctx = decode_keys(a, seq);
     }
@@ -434,55 +441,55 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
 
 // Folds the pieces of each (sequence, head) the balanced kernel split across
 // waves: w_p = 2^(lse_p - max lse), out = sum w_p o_p / sum w_p
-// (paged_kernels.py:574-629, in the log2 domain). One wave per (head,
-// sequence); a context no wave boundary cut was written directly.
+// (paged_kernels.py:574-629, in the log2 domain). One wave per (sequence,
+// head), reading the piece range the wave holding the context's first key
+// recorded; a context no wave boundary cut was written directly. Lane k
+// holds piece k's weight (64 pieces at a time) and the partial rows are read
+// eight pieces at a time so their loads overlap.
 template <typename T>
 __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   constexpr int kMaxC = kGenericMaxHeadDim / 64;
+  constexpr int kBatch = 8;
   const int lane = threadIdx.x;
   const int head = blockIdx.x % a.num_heads;
   const int seq = blockIdx.x / a.num_heads;
-  const int ctx = decode_keys(a, seq);
-  if (ctx == 0) return;
-  int64_t total, share;
-  balanced_share(a, total, share);
-  // Flattened offset of this (sequence, KV head).
-  int64_t before = 0;
-  for (int s0 = 0; s0 < seq; s0 += 64) {
-    const int s = s0 + lane;
-    before += (s < seq) ? (int64_t)decode_keys(a, s) : 0;
-  }
-  const int G = a.groups;
+  const int G = a.groups, D = a.head_dim;
   const int kvh = head / G, h = head % G;
-  const int64_t off = wave_sum_i64(before) * a.num_kv_heads + (int64_t)kvh * ctx;
-  const int64_t w0 = off / share, w1 = (off + ctx - 1) / share;
-  if (w0 == w1) return;
-  const int D = a.head_dim;
-  const int n = (int)(w1 - w0 + 1);
+  if (decode_keys(a, seq) == 0) return;
+  const int4 info = a.pieces[(int64_t)seq * a.num_kv_heads + kvh];
+  const int w0 = info.x, w1 = info.y, slot0 = info.z;
+  if (w1 <= w0) return;
+  const int n = w1 - w0 + 1;
+  auto row_of = [&](int j) -> int64_t { return ((int64_t)(w0 + j) * 2 + (j == 0 ? slot0 : 0)) * G + h; };
 
-  // Weights: lane j holds piece j, j + 64, ...
   float mx = -INFINITY;
-  for (int j = lane; j < n; j += 64) {
-    const int64_t w = w0 + j;
-    const int slot = (w * share >= off) ? 0 : 1;
-    mx = fmaxf(mx, a.part_lse[(w * 2 + slot) * G + h]);
-  }
+  for (int j = lane; j < n; j += 64) mx = fmaxf(mx, a.part_lse[row_of(j)]);
   mx = li_wave_max(mx);
   float acc[kMaxC];
 #pragma unroll
   for (int c = 0; c < kMaxC; ++c) acc[c] = 0.f;
   float wsum = 0.f;
-  for (int j = 0; j < n; ++j) {
-    const int64_t w = w0 + j;
-    const int slot = (w * share >= off) ? 0 : 1;
-    const int64_t r = (w * 2 + slot) * G + h;
-    const float wt = exp2f(a.part_lse[r] - mx);
-    wsum += wt;
-    const float* po = a.part_o + r * D;
+  for (int j0 = 0; j0 < n; j0 += 64) {
+    const int jn = min(64, n - j0);
+    const float wl = lane < jn ? exp2f(a.part_lse[row_of(j0 + lane)] - mx) : 0.f;
+    wsum += li_wave_sum(wl);
+    for (int kb = 0; kb < jn; kb += kBatch) {
+      float v[kBatch][kMaxC];
 #pragma unroll
-    for (int c = 0; c < kMaxC; ++c) {
-      const int d = lane + 64 * c;
-      if (d < D) acc[c] = fmaf(wt, po[d], acc[c]);
+      for (int k = 0; k < kBatch; ++k) {
+        const float* po = a.part_o + row_of(min(j0 + kb + k, n - 1)) * D;
+#pragma unroll
+        for (int c = 0; c < kMaxC; ++c) {
+          const int d = lane + 64 * c;
+          v[k][c] = (kb + k < jn && d < D) ? po[d] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const float wt = __shfl(wl, (kb + k) & 63, 64);
+#pragma unroll
+        for (int c = 0; c < kMaxC; ++c) acc[c] = fmaf(wt, v[k][c], acc[c]);
+      }
     }
   }
   const float inv = 1.f / wsum;

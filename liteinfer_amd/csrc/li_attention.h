@@ -39,6 +39,7 @@ struct AttnArgs {
   int num_qblocks;        // query blocks per sequence in the grid
   int max_query_len;      // most queries any sequence brings (prefill)
   int single_query_elsewhere;  // prefill: one-query sequences are served by the decode kernel
+  int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
 };
 
 // Largest head_dim the general-shape kernel serves.

@@ -77,18 +77,23 @@ int balanced_waves(int num_cus) {
   return std::max(1, num_cus) * per_cu;
 }
 
-size_t balanced_workspace(int waves, int groups, int head_dim) {
+size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads) {
   const size_t rows = (size_t)waves * 2 * groups;
-  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float));
+  return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) +
+         align256((size_t)batch * num_kv_heads * 16);
 }
 
-// Points a balanced launch's partial buffers into `workspace`.
+// Points a balanced launch's partial buffers and piece table into `workspace`.
 void set_balanced(AttnArgs& d, int waves, void* workspace) {
   d.num_parts = waves;
   d.part_len = -1;
   const size_t rows = (size_t)waves * 2 * d.groups;
-  d.part_o = static_cast<float*>(workspace);
-  d.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + align256(rows * d.head_dim * sizeof(float)));
+  char* p = static_cast<char*>(workspace);
+  d.part_o = reinterpret_cast<float*>(p);
+  p += align256(rows * d.head_dim * sizeof(float));
+  d.part_lse = reinterpret_cast<float*>(p);
+  p += align256(rows * sizeof(float));
+  d.pieces = reinterpret_cast<int4*>(p);
 }
 
 int check_common(int dtype, int num_heads, int num_kv_heads, int head_dim, const char* who) {
@@ -137,7 +142,7 @@ extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, 
   if (num_splits == 0) {
     // The MFMA kernel's automatic mode is the balanced split; size for either.
     if (num_cus <= 0) num_cus = device_cu_count();
-    need = std::max(need, balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim));
+    need = std::max(need, balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch, num_kv_heads));
   }
   if (workspace_bytes) *workspace_bytes = need;
   return LI_OK;
@@ -204,9 +209,9 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
     // Automatic mode on the MFMA kernel: the balanced split (it launches its
     // own combine).
     const int waves = balanced_waves(device_cu_count());
-    if (balanced_workspace(waves, a.groups, head_dim) > workspace_bytes || !workspace)
-      return fail(LI_EWORKSPACE, "li_paged_decode: workspace of %zu bytes given, %zu needed", workspace_bytes,
-                  balanced_workspace(waves, a.groups, head_dim));
+    const size_t bneed = balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads);
+    if (bneed > workspace_bytes || !workspace)
+      return fail(LI_EWORKSPACE, "li_paged_decode: workspace of %zu bytes given, %zu needed", workspace_bytes, bneed);
     set_balanced(a, waves, workspace);
     return launch_decode_mfma(a, dtype, s);
   }
@@ -222,7 +227,8 @@ extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
   if (int rc = check_common(LI_BF16, num_heads, num_kv_heads, head_dim, "li_paged_prefill_plan")) return rc;
   if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_prefill_plan: negative extent");
   if (num_cus <= 0) num_cus = device_cu_count();
-  if (workspace_bytes) *workspace_bytes = balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim);
+  if (workspace_bytes)
+    *workspace_bytes = balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch, num_kv_heads);
   return LI_OK;
 }
 
@@ -274,7 +280,7 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
     // work-group; the decode kernel serves them instead, its key axis cut
     // into partitions, and the prefill kernel skips them.
     const int waves = balanced_waves(device_cu_count());
-    const size_t need = balanced_workspace(waves, a.groups, head_dim);
+    const size_t need = balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads);
     if (!workspace || workspace_bytes < need)
       return fail(LI_EWORKSPACE, "li_paged_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
     AttnArgs d = a;
