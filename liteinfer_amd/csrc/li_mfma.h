@@ -106,6 +106,40 @@ __device__ __forceinline__ const T* row_ptr(const T* base, uint32_t row, uint32_
   return reinterpret_cast<const T*>(reinterpret_cast<uintptr_t>(base) + (uint64_t)row * row_bytes);
 }
 
+// An MFMA operand of all ones (bf16 / fp16 1.0): times P^T it gives every
+// output row the column sums of P^T, i.e. each query row's sum of weights.
+template <typename Frag>
+__device__ __forceinline__ Frag li_ones() {
+  typedef __attribute__((__vector_size__(8 * sizeof(uint16_t)))) uint16_t u16x8;
+  // 0x3f80 is 1.0 in bf16; 0x3c00 is 1.0 in fp16.
+  constexpr uint16_t one = sizeof(Frag) == 16 && __is_same(Frag, bf16x8_t) ? 0x3f80 : 0x3c00;
+  const u16x8 v = {one, one, one, one, one, one, one, one};
+  return __builtin_bit_cast(Frag, v);
+}
+
+// The V^T operand of O^T += V^T P^T for the 16 dims 16 blk .. 16 blk + 15,
+// read from a 32-key V tile in LDS (layout L) with two transposing LDS reads
+// (ds_read_b64_tr_b16, gfx950). Within a group of 16 lanes such a read gives
+// lane 4a + t the element t of the 8-byte reads of lanes a, a + 4, a + 8,
+// a + 12. So lane (s, g) reads dims 16 blk + 4 (s % 4) .. + 3 of key
+// 4g + s / 4 (then of key 16 + 4g + s / 4), and lane (m, g) receives dim
+// 16 blk + m of keys kappa(g, 0..7): its A operand, row m = that dim, with
+// the keys in the order the S^T blocks deliver the weights.
+template <typename L, typename Frag>
+__device__ __forceinline__ Frag li_read_vt(const char* vtile, int blk, int lane) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const int s = lane & 15, g = lane >> 4;
+  const int a = s & 3, j = s >> 2;
+  const int chunk = 2 * blk + (a >> 1);
+  const int byte = 8 * (a & 1);
+  const char* lo = vtile + L::offset(4 * g + j, chunk) + byte;
+  const char* hi = vtile + L::offset(16 + 4 * g + j, chunk) + byte;
+  const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(lo));
+  const v4s y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(hi));
+  const short __attribute__((ext_vector_type(8))) xy = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+  return __builtin_bit_cast(Frag, xy);
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(p);
 }

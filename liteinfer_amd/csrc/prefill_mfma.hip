@@ -75,7 +75,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   using Frag = typename M::Frag;
   using L = TileLayout<D>;
   constexpr int kSteps = D / 32;
-  constexpr int kChunks = D / 8;
   constexpr int kDmaPerStage = 2 * 2 * (L::kInsts / kWaves);
   __shared__ __attribute__((aligned(16))) int sl[kSlotChunk + kStageKeys];
   __shared__ __attribute__((aligned(1024))) char stages[2][2 * L::kTileBytes];
@@ -138,12 +137,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint32_t row_bytes = (uint32_t)(a.p_s0 * sizeof(T));
   const float sc = a.scale * kLog2eMfma;
 
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
-  floatx4_t acc[2][8];
+  // acc[nb][blk] for blk < D / 16: dims 16 blk + 4g .. of the lane's row;
+  // acc[nb][D / 16]: the row's softmax denominator, as the MFMA product of
+  // the weights with a block of ones (every element holds the same sum).
+  float m[2] = {-INFINITY, -INFINITY};
+  floatx4_t acc[2][D / 16 + 1];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[nb][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < D / 16 + 1; ++i) acc[nb][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  const Frag ones = li_ones<Frag>();
 
   // Folds the 32 keys of `tile` whose first key is t0 into both row blocks.
   auto fold = [&](const char* tile, int t0) {
@@ -190,13 +193,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const float mnew = (mx > m[nb] + kLazyRescale) ? mx : m[nb];
       alpha[nb] = __builtin_amdgcn_exp2f(m[nb] - mnew);
       rescale |= mnew != m[nb];
-      float psum = 0.f, p[8];
+      float p[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
-        psum += p[e];
-      }
-      l[nb] = l[nb] * alpha[nb] + psum;
+      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
       m[nb] = mnew;
       u32x4_t pw;
 #pragma unroll
@@ -207,35 +206,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < D / 16 + 1; ++i)
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[nb][i][r] *= alpha[nb];
     }
     __builtin_amdgcn_sched_barrier(0);
-    // O^T += V^T P^T, four dims of the chunk at a time.
+    // O^T += V^T P^T, 16 dims at a time. The V^T operand comes straight out
+    // of LDS through transposing reads (li_read_vt): lane (m, g) gets dim
+    // 16 blk + m of keys kappa(g, 0..7).
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      // Bytes 8 * half .. of each key's 16-byte chunk: dims 8n + 4 half ..
-      uint2 vr[8];
+    for (int blk = 0; blk < D / 16; ++blk) {
+      const Frag vf = li_read_vt<L, Frag>(vtile, blk, lane);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        vr[e] = (n < kChunks) ? *reinterpret_cast<const uint2*>(vtile + L::offset(kappa(g, e), n) + 8 * half)
-                              : uint2{0u, 0u};
-      }
-#pragma unroll
-      for (int i = 4 * half; i < 4 * half + 4; ++i) {
-        const int wd = (i >> 1) & 1;
-        u32x4_t va;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t lo = wd ? vr[2 * u].y : vr[2 * u].x, hi = wd ? vr[2 * u + 1].y : vr[2 * u + 1].x;
-          va[u] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-        }
-        const Frag vf = __builtin_bit_cast(Frag, va);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[nb][i] = M::mma(vf, pf[nb], acc[nb][i]);
-      }
+      for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf, pf[nb], acc[nb][blk]);
     }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) acc[nb][D / 16] = M::mma(ones, pf[nb], acc[nb][D / 16]);
   };
 
   for (int c0 = 0; c0 < kend; c0 += kSlotChunk) {
@@ -267,19 +253,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    const float lt = li_group_sum(l[nb]);
+    const float lt = acc[nb][D / 16][0];
     if (!real[nb]) continue;
     const float inv = 1.f / lt;
-    T* orow = static_cast<T*>(a.out) + (int64_t)tok[nb] * a.o_s0 + (int64_t)head[nb] * a.o_s1;
+    // acc[nb][blk][r] is dim 16 blk + 4 g + r of this lane's row.
+    T* orow = static_cast<T*>(a.out) + (int64_t)tok[nb] * a.o_s0 + (int64_t)head[nb] * a.o_s1 + 4 * g;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int chunk = 4 * g + r;
-      if (chunk < kChunks) {
-        u32x4_t wv;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) wv[u] = li_pack2<T>(acc[nb][2 * u][r] * inv, acc[nb][2 * u + 1][r] * inv);
-        *reinterpret_cast<u32x4_t*>(orow + 8 * chunk) = wv;
-      }
+    for (int blk = 0; blk < D / 16; ++blk) {
+      uint2 wv;
+      wv.x = li_pack2<T>(acc[nb][blk][0] * inv, acc[nb][blk][1] * inv);
+      wv.y = li_pack2<T>(acc[nb][blk][2] * inv, acc[nb][blk][3] * inv);
+      *reinterpret_cast<uint2*>(orow + 16 * blk) = wv;
     }
   }
 }
