@@ -234,7 +234,7 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "paged decode call (decode_mfma + combine_parts)",
+            "kernel": "paged decode call (decode_balanced + combine_balanced)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
