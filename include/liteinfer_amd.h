@@ -125,7 +125,8 @@ int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
  * Workspace bytes li_paged_prefill needs for a pass of `batch` sequences over
  * a slot table `max_context` wide on a device of `num_cus` compute units
  * (0 = ask the current device): partials of its one-query sequences, which
- * the decode kernel serves with a partitioned key axis. No counterpart in
+ * the decode kernel serves with a partitioned key axis, and the list that
+ * orders the prefill kernel's query blocks longest first. No counterpart in
  * the reference, whose prefill kernel allocates nothing
  * (liteinfer/models/paged_kernels.py:867).
  */

@@ -38,8 +38,10 @@ struct AttnArgs {
   int block_q, block_kv;  // general-shape kernel tiles
   int num_qblocks;        // query blocks per sequence in the grid
   int max_query_len;      // most queries any sequence brings (prefill)
+  int max_context;        // slot-table width (prefill)
   int single_query_elsewhere;  // prefill: one-query sequences are served by the decode kernel
   int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
+  int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
 };
 
 // Largest head_dim the general-shape kernel serves.
@@ -57,5 +59,8 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s);
 // MFMA prefill: same applicability rules as decode.
 bool prefill_mfma_applies(const AttnArgs& a, int dtype);
 int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t s);
+// Entries of the MFMA prefill work list for a pass over a slot table
+// max_context wide: an upper bound on its query blocks.
+size_t prefill_work_entries(int batch, int max_context);
 
 }  // namespace li

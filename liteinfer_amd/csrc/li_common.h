@@ -71,10 +71,12 @@ __device__ __forceinline__ li_f16 li_from_float<li_f16>(float x) { return (li_f1
 // rounded to nearest even.
 template <typename T>
 __device__ __forceinline__ uint32_t li_pack2(float lo, float hi) {
-  T a = li_from_float<T>(lo), b = li_from_float<T>(hi);
-  uint16_t ua = __builtin_bit_cast(uint16_t, a);
-  uint16_t ub = __builtin_bit_cast(uint16_t, b);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
+  // A two-element vector conversion, so a single packed convert
+  // (v_cvt_pk_bf16_f32 on gfx950) does both roundings.
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  const t2 v = __builtin_convertvector((f2){lo, hi}, t2);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // Wave64 reductions. Every lane gets the result.

@@ -221,6 +221,13 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
   return rc;
 }
 
+// Workspace of the MFMA prefill path: the balanced decode kernel's partials
+// for the one-query sequences, then the prefill work list.
+size_t prefill_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads, int max_context) {
+  return balanced_workspace(waves, groups, head_dim, batch, num_kv_heads) +
+         align256(prefill_work_entries(batch, max_context) * sizeof(int));
+}
+
 extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,
                                      int num_cus, size_t* workspace_bytes) {
   clear_error();
@@ -228,7 +235,8 @@ extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
   if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_prefill_plan: negative extent");
   if (num_cus <= 0) num_cus = device_cu_count();
   if (workspace_bytes)
-    *workspace_bytes = balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch, num_kv_heads);
+    *workspace_bytes = prefill_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch,
+                                         num_kv_heads, max_context);
   return LI_OK;
 }
 
@@ -272,6 +280,7 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
   a.part_len = 0;
   a.block_kv = block_kv > 0 ? block_kv : kDefaultBlockKv;
   a.max_query_len = max_query_len;
+  a.max_context = max_context;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!(flags & LI_FLAG_FORCE_GENERIC) && prefill_mfma_applies(a, dtype)) {
@@ -280,9 +289,11 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
     // work-group; the decode kernel serves them instead, its key axis cut
     // into partitions, and the prefill kernel skips them.
     const int waves = balanced_waves(device_cu_count());
-    const size_t need = balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads);
+    const size_t need = prefill_workspace(waves, a.groups, head_dim, batch, num_kv_heads, max_context);
     if (!workspace || workspace_bytes < need)
       return fail(LI_EWORKSPACE, "li_paged_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
+    a.work = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+                                    balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads));
     AttnArgs d = a;
     d.block_q = 1;
     d.num_qblocks = 1;

@@ -19,21 +19,24 @@
 //   S^T = K Q^T     A = K rows from LDS, B = the rows' Q^T kept in registers.
 //                   Lane (n, g) gets the scores of keys {4g..4g+3,
 //                   16+4g..16+4g+3} for row n.
-//   O^T += V^T P^T  B = P^T is those 8 weights as they are; A = V^T is 8
-//                   16-byte V chunks (dims 8n.., the same 8 keys) from LDS
-//                   turned into 8 operands by a register-only 8x8 transpose,
-//                   shared by both row blocks.
+//   O^T += V^T P^T  B = P^T is those 8 weights as they are; A = V^T comes
+//                   straight out of LDS through transposing reads
+//                   (ds_read_b64_tr_b16, li_read_vt), shared by both row
+//                   blocks. One more MFMA against a block of ones gives each
+//                   row's sum of weights.
 //
 // A row's visibility is key <= its position; the mask is a compare per
-// score, applied on every tile (it is all-true before the block's first
-// query). Padding rows (past the block or the sequence) see every key with a
-// zero query, so they stay finite, and are never stored.
+// score, applied only to tiles that reach past the block's first query
+// position (the diagonal). Padding rows (past the block or the sequence) see
+// every key with a zero query, so they stay finite, and are never stored.
 //
-// Grid order: the (sequence, KV head) pair is the fastest index, so with
-// num_kv_heads a multiple of 8 every query block of a pair lands on the same
-// XCD (work-groups are dealt to the 8 XCDs round robin) and reuses its K/V
-// from that XCD's L2; the last query blocks, which see the most keys, are
-// dispatched first.
+// Grid order: work-group i takes query block work[i / num_kv_heads] (a list
+// prefill_order sorts longest first) and KV head i % num_kv_heads. Work-groups
+// are dispatched in grid order as earlier ones retire, so the longest blocks
+// start first and short ones fill in behind them; and with num_kv_heads a
+// multiple of 8 every block of one KV head lands on the same XCD
+// (work-groups are dealt to the 8 XCDs round robin) and reuses that head's
+// K/V from the XCD's L2.
 #include "li_attention.h"
 #include "li_mfma.h"
 
@@ -84,11 +87,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
   const int n = lane & 15, g = lane >> 4;
 
-  const int pairs = a.batch * a.num_kv_heads;
-  const int pair = blockIdx.x % pairs;
-  const int qblock = a.num_qblocks - 1 - (int)(blockIdx.x / pairs);
-  const int seq = pair / a.num_kv_heads;
-  const int kvh = pair % a.num_kv_heads;
+  const int item = a.work[blockIdx.x / a.num_kv_heads];
+  if (item < 0) return;  // past the list's end
+  const int seq = item / a.num_qblocks;
+  const int qblock = item % a.num_qblocks;
+  const int kvh = blockIdx.x % a.num_kv_heads;
 
   const int first_tok = a.qsl[seq];
   const int nq = a.qsl[seq + 1] - first_tok;
@@ -268,11 +271,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// Work list of the prefill grid: every non-empty query block
+// (sequence * num_qblocks + block) ordered by the number of 32-key tiles it
+// folds, most first (a counting sort on tiles >> shift), then -1 up to
+// batch * num_qblocks. Work-groups are dispatched in grid order as earlier
+// ones retire, so this is longest-processing-time-first scheduling: the
+// long blocks start at once and the short ones fill in behind them. One
+// work-group; the order within a bucket is whatever the LDS atomics give,
+// which changes the schedule only, never a result.
+constexpr int kOrderBins = 256;
+
+__global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
+  __shared__ int hist[kOrderBins];
+  __shared__ int max_tiles;
+  const int tid = threadIdx.x;
+  const int items = a.batch * a.num_qblocks;
+  auto tiles_of = [&](int it) {
+    const int seq = it / a.num_qblocks, qb = it % a.num_qblocks;
+    const int first = a.qsl[seq];
+    const int nq = a.qsl[seq + 1] - first;
+    const int q0 = qb * a.block_q;
+    if (q0 >= nq || (nq == 1 && a.single_query_elsewhere)) return 0;
+    const int kend = a.ctx[seq] - nq + min(q0 + a.block_q, nq);
+    return (kend + 31) / 32;
+  };
+  if (tid < kOrderBins) hist[tid] = 0;
+  if (tid == 0) max_tiles = 0;
+  __syncthreads();
+  int local = 0;
+  for (int it = tid; it < items; it += 1024) local = max(local, tiles_of(it));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) local = max(local, __shfl_xor(local, off, 64));
+  if ((tid & 63) == 0) atomicMax(&max_tiles, local);
+  __syncthreads();
+  int shift = 0;
+  while ((max_tiles >> shift) >= kOrderBins) ++shift;
+  // Bin b holds blocks of (tiles >> shift) == kOrderBins - 1 - b, so bins
+  // run from the heaviest down.
+  for (int it = tid; it < items; it += 1024) {
+    const int t = tiles_of(it);
+    if (t > 0) atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], 1);
+  }
+  __syncthreads();
+  // Exclusive prefix sum over the bins: Hillis-Steele in LDS.
+  int v = tid < kOrderBins ? hist[tid] : 0;
+  const int own = v;
+#pragma unroll
+  for (int d = 1; d < kOrderBins; d *= 2) {
+    __syncthreads();
+    const int add = (tid < kOrderBins && tid >= d) ? hist[tid - d] : 0;
+    __syncthreads();
+    v += add;
+    if (tid < kOrderBins) hist[tid] = v;
+  }
+  __syncthreads();
+  if (tid < kOrderBins) hist[tid] = v - own;
+  if (tid == kOrderBins - 1) max_tiles = v;  // now: the number of blocks listed
+  __syncthreads();
+  for (int it = tid; it < items; it += 1024) {
+    const int t = tiles_of(it);
+    if (t > 0) a.work[atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], 1)] = it;
+  }
+  for (int i = max_tiles + tid; i < items; i += 1024) a.work[i] = -1;
+}
+
 bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
   return aligned16(p) && (s0 * esize) % 16 == 0 && (s1 * esize) % 16 == 0;
 }
 
 }  // namespace
+
+size_t prefill_work_entries(int batch, int max_context) {
+  // A sequence's queries are the last of its context, so it has at most
+  // max_context of them; blocks hold at least kRows / 16 query tokens.
+  return (size_t)batch * cdiv(max(max_context, 1), kRows / 16);
+}
 
 bool prefill_mfma_applies(const AttnArgs& a, int dtype) {
   if (dtype != LI_BF16 && dtype != LI_F16) return false;
@@ -289,6 +362,10 @@ int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) {
   const int64_t blocks = (int64_t)a.batch * a.num_kv_heads * a.num_qblocks;
   if (blocks == 0) return LI_OK;
   if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "prefill grid of %lld blocks is too large", (long long)blocks);
+  if ((size_t)a.batch * a.num_qblocks > prefill_work_entries(a.batch, a.max_context))
+    return fail(LI_EINVAL, "prefill: %d query blocks per sequence exceed the planned work list", a.num_qblocks);
+  hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
+  if (int rc = check_launch("prefill_order")) return rc;
   const dim3 grid((unsigned)blocks), block(256);
   if (dtype == LI_BF16) {
     if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128>), grid, block, 0, s, a);
