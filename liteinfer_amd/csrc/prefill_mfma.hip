@@ -152,10 +152,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const Frag ones = li_ones<Frag>();
 
   // Folds the 32 keys of `tile` whose first key is t0 into both row blocks.
-  auto fold = [&](const char* tile, int t0) {
+  auto fold = [&](const char* tile, int t0) __attribute__((always_inline)) {
     const char* vtile = tile + 32 * L::kRowBytes;
     // S^T, one 16-key block at a time so only its K operands are live.
     floatx4_t s[2][2];
+    // Raised priority while this wave issues MFMAs, so the SIMD's other
+    // wave's vector work fills in around them rather than the reverse.
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
       Frag kf[kSteps];
@@ -169,6 +172,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
     // Online softmax per row block; the scale is folded into the exponent.
     Frag pf[2];
     float alpha[2];
@@ -214,6 +218,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           for (int r = 0; r < 4; ++r) acc[nb][i][r] *= alpha[nb];
     }
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
     // O^T += V^T P^T, 16 dims at a time. The V^T operand comes straight out
     // of LDS through transposing reads (li_read_vt): lane (m, g) gets dim
     // 16 blk + m of keys kappa(g, 0..7).
@@ -225,6 +230,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) acc[nb][D / 16] = M::mma(ones, pf[nb], acc[nb][D / 16]);
+    __builtin_amdgcn_s_setprio(0);
   };
 
   for (int c0 = 0; c0 < kend; c0 += kSlotChunk) {
