@@ -56,6 +56,13 @@ __device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ k
   using L = TileLayout<D>;
   constexpr int kPerWave = L::kInsts / kWaves;
   const int rr = lane / L::kCh, nn = lane % L::kCh;
+  // All slot reads first: each load below is an asm statement with a memory
+  // clobber, so a read placed after one would wait for its own round trip.
+  uint32_t slot[2][kPerWave];
+#pragma unroll
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int ii = 0; ii < kPerWave; ++ii) slot[half][ii] = (uint32_t)sl[t + 32 * half + rr * L::kInsts + w * kPerWave + ii];
 #pragma unroll
   for (int half = 0; half < 2; ++half) {
     char* tile = stage + half * L::kTileBytes;
@@ -63,11 +70,10 @@ __device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ k
     for (int ii = 0; ii < kPerWave; ++ii) {
       const int i = w * kPerWave + ii;
       const int key = rr * L::kInsts + i;
-      const uint32_t slot = (uint32_t)sl[t + 32 * half + key];
       const int chunk = nn ^ (key % L::kCh);
       const uint32_t dst = lds_addr(tile + i * 1024);
-      dma16(row_ptr(kpool + 8 * chunk, slot, row_bytes), dst);
-      dma16(row_ptr(vpool + 8 * chunk, slot, row_bytes), dst + 32 * L::kRowBytes);
+      dma16(row_ptr(kpool + 8 * chunk, slot[half][ii], row_bytes), dst);
+      dma16(row_ptr(vpool + 8 * chunk, slot[half][ii], row_bytes), dst + 32 * L::kRowBytes);
     }
   }
 }
