@@ -50,8 +50,14 @@ enum li_status {
 /* Flags for li_paged_decode / li_paged_prefill. */
 enum li_flags {
   LI_FLAG_NONE = 0,
-  LI_FLAG_FORCE_GENERIC = 1 /* run the general-shape kernel even where the
+  LI_FLAG_FORCE_GENERIC = 1, /* run the general-shape kernel even where the
                                MFMA kernel applies (used by the parity tests) */
+  LI_FLAG_EQUAL_SPLITS = 2   /* li_paged_decode on the MFMA kernel: honour
+                               num_splits >= 1 as the reference's equal-slice
+                               partition count. Without it the MFMA kernel
+                               takes num_splits as a scheduling hint only and
+                               runs its balanced split (the same attention,
+                               within fp32 rounding of the partial combine) */
 };
 
 /* Message of the last failure on this thread ("" if none). */
@@ -88,12 +94,13 @@ int li_choose_num_splits(int batch, int num_kv_heads, int max_context,
                          int num_cus, int block_kv);
 
 /*
- * The launch plan of li_paged_decode: how many partitions the grid holds,
- * how long each one is (0 = each sequence's context cut into num_partitions
- * equal slices, the reference's split rule, paged_kernels.py:495-498), and
- * how many workspace bytes the call needs. num_splits = 0 chooses (fixed
- * length partitions, so a long context is cut more finely than a short one);
- * num_splits >= 1 pins the reference's equal-slice split.
+ * The launch plan of li_paged_decode's partitioned schedule: how many
+ * partitions the grid holds, how long each one is (0 = each sequence's
+ * context cut into num_partitions equal slices, the reference's split rule,
+ * paged_kernels.py:495-498), and how many workspace bytes the call needs
+ * under any schedule it may run (the MFMA kernel's balanced split included).
+ * num_splits = 0 chooses (fixed-length partitions, so a long context is cut
+ * more finely than a short one); num_splits >= 1 is the equal-slice split.
  */
 int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads,
                          int head_dim, int max_context, int num_splits,

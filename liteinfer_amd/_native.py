@@ -19,6 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libliteinfer_amd.so"
 LI_F32, LI_F16, LI_BF16 = 0, 1, 2
 LI_OK, LI_EINVAL, LI_EUNSUPPORTED, LI_ELAUNCH, LI_EWORKSPACE = 0, -1, -2, -3, -4
 LI_FLAG_FORCE_GENERIC = 1
+LI_FLAG_EQUAL_SPLITS = 2
 
 DTYPE_CODES = {torch.float32: LI_F32, torch.float16: LI_F16, torch.bfloat16: LI_BF16}
 

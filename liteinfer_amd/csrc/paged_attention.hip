@@ -139,11 +139,10 @@ extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, 
   if (num_partitions) *num_partitions = parts;
   if (partition_len) *partition_len = plen;
   size_t need = decode_workspace(batch, num_heads, head_dim, parts);
-  if (num_splits == 0) {
-    // The MFMA kernel's automatic mode is the balanced split; size for either.
-    if (num_cus <= 0) num_cus = device_cu_count();
-    need = std::max(need, balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch, num_kv_heads));
-  }
+  // The MFMA kernel runs the balanced split unless LI_FLAG_EQUAL_SPLITS pins
+  // the partitions; size for either.
+  if (num_cus <= 0) num_cus = device_cu_count();
+  need = std::max(need, balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch, num_kv_heads));
   if (workspace_bytes) *workspace_bytes = need;
   return LI_OK;
 }
@@ -205,9 +204,11 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool mfma = !(flags & LI_FLAG_FORCE_GENERIC) && decode_mfma_applies(a, dtype);
-  if (mfma && num_splits == 0) {
-    // Automatic mode on the MFMA kernel: the balanced split (it launches its
-    // own combine).
+  if (mfma && (num_splits == 0 || !(flags & LI_FLAG_EQUAL_SPLITS))) {
+    // The MFMA kernel's schedule: the balanced split (it launches its own
+    // combine). A split count the caller chose (the engine passes
+    // choose_num_splits's) is a scheduling hint; LI_FLAG_EQUAL_SPLITS makes
+    // it the partition count.
     const int waves = balanced_waves(device_cu_count());
     const size_t bneed = balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads);
     if (bneed > workspace_bytes || !workspace)

@@ -49,13 +49,19 @@ _MAX_SPLITS = 1024
 # Compute units assumed when no device is visible (MI355X: 8 XCDs x 32 CUs).
 _MI355X_COMPUTE_UNITS = 256
 
-_KERNELS = ("auto", "generic")
+_KERNELS = ("auto", "generic", "equal_splits")
 
 
 def _flags(kernel: str) -> int:
     if kernel not in _KERNELS:
         raise ValueError(f"kernel must be one of {_KERNELS}, got {kernel!r}")
-    return _native.LI_FLAG_FORCE_GENERIC if kernel == "generic" else 0
+    return {"auto": 0, "generic": _native.LI_FLAG_FORCE_GENERIC, "equal_splits": _native.LI_FLAG_EQUAL_SPLITS}[kernel]
+
+
+def _prefill_kernel(kernel: str) -> str:
+    if kernel not in ("auto", "generic"):
+        raise ValueError(f"kernel must be one of ('auto', 'generic'), got {kernel!r}")
+    return kernel
 
 
 @functools.cache
@@ -188,10 +194,16 @@ def paged_decode(
         num_kv_groups: query heads per KV head.
         block_kv: key tile of the general-shape kernel and the granularity of
             the chosen partitions.
-        num_splits: ``None`` lets `choose_num_splits` cut the key axis into
-            fixed-length partitions; an integer pins the reference's rule, each
-            sequence's context cut into that many equal slices.
-        kernel: ``"auto"`` (MFMA where it applies) or ``"generic"``.
+        num_splits: how many slices each sequence's keys are cut into. On the
+            MFMA kernel (bf16 / fp16) this is a scheduling hint: it runs its
+            balanced split, equal keys per wave across the whole batch, for
+            any value. On the general-shape kernel, and on the MFMA kernel
+            with ``kernel="equal_splits"``, an integer is the reference's rule
+            (each context cut into that many equal slices) and ``None`` picks
+            fixed-length partitions. The result is the same attention either
+            way, within fp32 rounding of the partial combine.
+        kernel: ``"auto"`` (MFMA where it applies), ``"generic"`` (the
+            general-shape kernel) or ``"equal_splits"`` (MFMA, splits pinned).
 
     Returns:
         ``[batch, num_heads, head_dim]``, same dtype as ``query``.
@@ -325,7 +337,7 @@ def paged_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
         num_heads, num_kv_heads, head_dim, float(scaling), block_q, block_kv,
         workspace.data_ptr() if workspace is not None else None, need.value,
-        _native.dtype_code(query.dtype), _flags(kernel), _native.stream_handle(device),
+        _native.dtype_code(query.dtype), _flags(_prefill_kernel(kernel)), _native.stream_handle(device),
     )
     _native.check(status, "paged_prefill")
     return out

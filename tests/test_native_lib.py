@@ -91,7 +91,21 @@ def test_plan_pins_the_reference_split_rule_when_asked():
     status, parts, plen, _ = _plan(num_splits=5)
     assert (status, parts, plen) == (0, 5, 0)
     status, parts, _, need = _plan(num_splits=1)
-    assert (status, parts, need) == (0, 1, 0)
+    assert (status, parts) == (0, 1)
+    # The MFMA kernel may still run its balanced split (a pinned count is a
+    # hint there): 4 waves per CU, two fp32 partials of G = 4 heads each.
+    assert need >= 256 * 4 * 2 * 4 * (128 + 1) * 4
+
+
+def test_kernel_choices_map_to_flags():
+    from liteinfer_amd.paged_kernels import _flags, _prefill_kernel
+    assert _flags("auto") == 0
+    assert _flags("generic") == _native.LI_FLAG_FORCE_GENERIC
+    assert _flags("equal_splits") == _native.LI_FLAG_EQUAL_SPLITS
+    with pytest.raises(ValueError):
+        _flags("fast")
+    with pytest.raises(ValueError):
+        _prefill_kernel("equal_splits")
 
 
 def test_plan_rejects_bad_arguments_with_a_message():

@@ -75,15 +75,15 @@ def test_splits_past_a_short_context_contribute_nothing():
 
 def test_padding_columns_are_never_read():
     b = PagedBatch([200, 65, 3], dtype=torch.bfloat16)
-    for kernel in ("auto", "generic"):
-        first = _run(b, kernel=kernel)
+    for kernel in ("auto", "equal_splits", "generic"):
+        first = _run(b, kernel=kernel, num_splits=3 if kernel == "equal_splits" else None)
         table = b.slot_table.clone()
         cols = torch.arange(table.shape[1], device=table.device)
         pad = cols[None, :] >= b.context_lens_t[:, None]
         table[pad] = torch.randint(1, 512, (int(pad.sum()),), device=table.device)
         b2 = b
         b2.slot_table = table
-        assert torch.equal(_run(b2, kernel=kernel), first)
+        assert torch.equal(_run(b2, kernel=kernel, num_splits=3 if kernel == "equal_splits" else None), first)
 
 
 def test_pools_laid_out_differently_are_refused():
@@ -102,7 +102,7 @@ def test_fewer_than_one_split_is_refused():
 # --- bf16 / fp16 through both kernels --------------------------------------------------
 
 
-@pytest.mark.parametrize("kernel", ["auto", "generic"])
+@pytest.mark.parametrize("kernel", ["auto", "equal_splits", "generic"])
 @pytest.mark.parametrize("num_splits", [None, 1, 11])
 def test_bfloat16_within_rounding(kernel, num_splits):
     b = PagedBatch([300, 129, 7], dtype=torch.bfloat16)
@@ -117,8 +117,9 @@ def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads):
     b = PagedBatch([1, 31, 32, 33, 100, 257, 1000], dtype=dtype, num_heads=num_heads, num_kv_heads=num_kv_heads,
                    head_dim=head_dim, num_slots=4096, seed=2)
     want = b.oracle()
-    for splits in (None, 1, 3):
-        assert_within(_run(b, num_splits=splits), want, 2 ** -6, 2e-3)
+    for kernel in ("auto", "equal_splits"):
+        for splits in (None, 1, 3):
+            assert_within(_run(b, kernel=kernel, num_splits=splits), want, 2 ** -6, 2e-3)
 
 
 def test_mfma_and_general_kernels_agree():
