@@ -84,6 +84,34 @@ int li_kv_scatter(const void* k, const void* v, const int64_t* k_strides,
                   int dtype, void* stream);
 
 /*
+ * Fused rotary embedding + KV slot-write. Replaces, per layer, the
+ * reference's _apply_rotary_pos_emb (liteinfer/models/llama.py:85-98, called
+ * at :155-156) followed by payload.update -> KVCache.scatter (llama.py:160,
+ * liteinfer/cache/kv_cache.py:236-253):
+ *     q_out = q * cos + rotate_half(q) * sin
+ *     key_pool[slots]   = tokens_first(k * cos + rotate_half(k) * sin)
+ *     value_pool[slots] = tokens_first(v)
+ * rotate_half(x) = cat(-x[..., D/2:], x[..., :D/2]). q / q_out are
+ * [batch, num_heads, tokens, head_dim], k / v [batch, num_kv_heads, tokens,
+ * head_dim], all with arbitrary element strides {batch, head, token, dim};
+ * cos / sin are [batch, tokens, head_dim] with strides cs_strides (stride 0
+ * broadcasts). slots holds batch*tokens entries in batch-major token order.
+ * Every product and sum is rounded to `dtype` as the separate torch ops round
+ * it, so q_out and the pool rows are bit-identical to the reference's
+ * sequence. A slot outside [0, num_slots) is not written.
+ */
+int li_rope_kv_write(const void* q, const int64_t* q_strides, const void* k,
+                     const int64_t* k_strides, const void* v,
+                     const int64_t* v_strides, const void* cos, const void* sin,
+                     const int64_t* cs_strides, int64_t batch, int64_t tokens,
+                     const int64_t* slots, void* q_out,
+                     const int64_t* q_out_strides, void* key_pool,
+                     void* value_pool, int64_t num_slots,
+                     int64_t pool_stride_slot, int64_t pool_stride_head,
+                     int num_heads, int num_kv_heads, int head_dim, int dtype,
+                     void* stream);
+
+/*
  * How many partitions each sequence's key loop is cut into for a decode step
  * of `batch` rows over a slot table `max_context` wide, on a device of
  * `num_cus` compute units (0 = ask the current device). Counterpart of

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "li_last_error_string",
     "li_abi_version",
     "li_kv_scatter",
+    "li_rope_kv_write",
     "li_choose_num_splits",
     "li_paged_decode_plan",
     "li_paged_decode",
@@ -44,6 +45,11 @@ _SIGNATURES = {
     "li_kv_scatter": (
         _i32,
         [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p],
+    ),
+    "li_rope_kv_write": (
+        _i32,
+        [_p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64p, _i64, _i64, _p, _p, _i64p, _p, _p,
+         _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p],
     ),
     "li_choose_num_splits": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "li_paged_decode_plan": (
@@ -64,7 +70,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

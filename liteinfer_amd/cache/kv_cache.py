@@ -128,6 +128,24 @@ class KVCache:
         keys, values = self._pool.slots(layer_idx)
         scatter_into(keys, values, slots, k, v)
 
+    def rotate_and_scatter(self, layer_idx: int, slots: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                           v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        """RoPE on q and k, then `scatter` of k and v; returns the rotated q.
+
+        One HIP launch on a ROCm device (`rope.rope_kv_write`); the torch ops
+        of llama.py:85-98 and `scatter` on the CPU.
+        """
+        keys, values = self._pool.slots(layer_idx)
+        if keys.device.type == "cuda":
+            from liteinfer_amd.rope import rope_kv_write
+
+            return rope_kv_write(q, k, v, cos, sin, slots, keys, values)
+        from liteinfer_amd.rope import apply_rotary_pos_emb
+
+        q_embed, k_embed = apply_rotary_pos_emb(q, k, cos, sin)
+        scatter_into(keys, values, slots, k_embed, v)
+        return q_embed
+
 
 class _PackedPayload:
     """A pass packed end to end: whole prompts, chunks and sampled tokens (kv_cache.py:256-293)."""
@@ -142,6 +160,16 @@ class _PackedPayload:
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> PagedKV:
         self._cache.scatter(layer_idx, self.addresses.slots, key_states, value_states)
+        return self._paged_kv(layer_idx)
+
+    def update_rotated(self, query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
+                       cos: torch.Tensor, sin: torch.Tensor, layer_idx: int) -> tuple[torch.Tensor, PagedKV]:
+        """`update` with the layer's RoPE fused in: returns (rotated q, PagedKV)."""
+        q = self._cache.rotate_and_scatter(layer_idx, self.addresses.slots, query_states, key_states, value_states,
+                                           cos, sin)
+        return q, self._paged_kv(layer_idx)
+
+    def _paged_kv(self, layer_idx: int) -> PagedKV:
         key_pool, value_pool = self._cache.layer_storage(layer_idx)
         return PagedKV(
             key_pool,
@@ -168,5 +196,15 @@ class _DecodePayload:
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int) -> PagedKV:
         self._cache.scatter(layer_idx, self._write_slots, key_states, value_states)
+        return self._paged_kv(layer_idx)
+
+    def update_rotated(self, query_states: torch.Tensor, key_states: torch.Tensor, value_states: torch.Tensor,
+                       cos: torch.Tensor, sin: torch.Tensor, layer_idx: int) -> tuple[torch.Tensor, PagedKV]:
+        """`update` with the layer's RoPE fused in: returns (rotated q, PagedKV)."""
+        q = self._cache.rotate_and_scatter(layer_idx, self._write_slots, query_states, key_states, value_states,
+                                           cos, sin)
+        return q, self._paged_kv(layer_idx)
+
+    def _paged_kv(self, layer_idx: int) -> PagedKV:
         key_pool, value_pool = self._cache.layer_storage(layer_idx)
         return PagedKV(key_pool, value_pool, self._slots, self._context_lens, self._num_splits)

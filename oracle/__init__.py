@@ -15,6 +15,9 @@ Modules:
               numpy float dtype (float64 is the reference answer).
   baseline    the dense eager / sdpa attention in torch fp32 on CPU threads,
               timed by bench.py as the CPU baseline.
+  rope        rotary embedding with the reference's per-op roundings and the
+              fused RoPE + slot-write (liteinfer/models/llama.py:79-98,
+              :155-160).
 
 How each function is pinned (tests/test_oracle.py):
   addressing.*        the reference's own known-answer vectors
@@ -32,4 +35,13 @@ How each function is pinned (tests/test_oracle.py):
                       query heads h with h // groups == that head; chunk rows
                       equal the same rows of the whole prompt.
   baseline.*          agrees with attention.attend to fp32 rounding.
+  rope.round_to       numpy's float16 conversion and, for bf16, torch's
+                      float32 -> bfloat16 conversion on every float32 bit
+                      pattern class (ties, carries into the exponent).
+  rope.rope           torch's CPU ops x * cos + rotate_half(x) * sin in the
+                      same dtype, bit for bit; exact cases: zero angle gives
+                      x, a quarter turn gives rotate_half(x); in float64 each
+                      (x[i], x[i + D/2]) pair keeps its length and two
+                      rotations compose into the rotation by the sum of
+                      their angles.
 """
