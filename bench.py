@@ -13,7 +13,9 @@ and outputs, and the slot-write's reads and writes. `roofline` rates the
 decode call (the partition kernel plus the partition combine, timed with HIP
 events on the stream they run on) against MI355X's 8 TB/s. Config 3's packed
 prefill (TFLOP/s of visible causal pairs) and config 4's long-context decode
-are reported beside it. `cpu_baseline` times the dense eager attention
+are reported beside it, and so is the fused RoPE + slot-write at config 3's
+packed pass and config 2's decode step, with the reference's separate torch
+ops timed on the same inputs. `cpu_baseline` times the dense eager attention
 (oracle/baseline.py) in fp32 on this host's cores over a bounded sample of the
 same step.
 
@@ -108,6 +110,57 @@ def _time_prefill(step, steps, warmup):
         b.record(stream)
     torch.cuda.synchronize()
     return [a.elapsed_time(b) for a, b in marks]
+
+
+def _time_rope(batch, tokens, geo, iters=50, num_slots=1 << 20, seed=0):
+    """Fused RoPE + slot-write vs the reference's separate torch ops (rotary, permute, index_put_)."""
+    from liteinfer_amd.rope import apply_rotary_pos_emb, rope_kv_write
+    from liteinfer_amd.cache.kv_cache import tokens_first
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    hq, hkv, d = geo.num_heads, geo.num_kv_heads, geo.head_dim
+    proj = lambda h: torch.randn(batch, tokens, h, d, generator=g, device="cuda").to(torch.bfloat16).transpose(1, 2)
+    q, k, v = proj(hq), proj(hkv), proj(hkv)
+    pos = torch.randint(0, 8192, (batch, tokens), generator=g, device="cuda").float()
+    inv = 1.0 / (500000.0 ** (torch.arange(0, d, 2, device="cuda").float() / d))
+    emb = torch.cat((pos[..., None] * inv, pos[..., None] * inv), dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    kp = torch.zeros(num_slots, hkv, d, dtype=torch.bfloat16, device="cuda")
+    vp = torch.zeros_like(kp)
+    slots = torch.randperm(num_slots, generator=torch.Generator().manual_seed(seed))[: batch * tokens].view(1, -1).cuda()
+
+    def unfused():
+        q_embed, k_embed = apply_rotary_pos_emb(q, k, cos, sin)
+        flat = slots.reshape(-1)
+        kp[flat] = tokens_first(k_embed)
+        vp[flat] = tokens_first(v)
+        return q_embed
+
+    def timed(fn):
+        for _ in range(5):
+            fn()
+        stream = torch.cuda.current_stream()
+        marks = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+        torch.cuda.synchronize()
+        for a, b in marks:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        return statistics.mean(a.elapsed_time(b) for a, b in marks) * 1e3
+
+    fused_us = timed(lambda: rope_kv_write(q, k, v, cos, sin, slots, kp, vp))
+    unfused_us = timed(unfused)
+    n = batch * tokens
+    nbytes = n * (2 * 2 * hq * d + 2 * 2 * 2 * hkv * d + 2 * 2 * d + 8)
+    return {
+        "tokens": n,
+        "avg_us": round(fused_us, 2),
+        "GB/s": round(nbytes / (fused_us * 1e-6) / 1e9, 1),
+        "frac_hbm": round(nbytes / (fused_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes": nbytes,
+        "unfused_torch_ops_us": round(unfused_us, 2),
+    }
 
 
 def cpu_baseline(step, max_seconds: float = 20.0) -> dict:
@@ -273,8 +326,12 @@ def main() -> int:
             "visible_pair_flops": flops,
             "query_tokens": sum(c3.host_query_lens),
         }
-        result["secondary"] = secondary
+        geo3, c3_tokens = c3.geometry, sum(c3.host_query_lens)
         del c3
+        torch.cuda.empty_cache()
+        secondary["rope_kv_write_c3"] = _time_rope(1, c3_tokens, geo3)
+        secondary["rope_kv_write_c2"] = _time_rope(64, 1, geo3)
+        result["secondary"] = secondary
         torch.cuda.empty_cache()
         step = None
 

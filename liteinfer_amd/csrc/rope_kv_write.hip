@@ -85,21 +85,24 @@ __device__ __forceinline__ void rotate(E lo, E hi, E c_lo, E s_lo, E c_hi, E s_h
 
 // Vector path: every row 16-byte aligned, head_dim a multiple of 2 * (16 /
 // sizeof(E)), unit dim strides.
-template <typename E>
+// I: the index type of the work-item arithmetic (32-bit whenever the total
+// fits, which spares the 64-bit division sequences).
+template <typename E, typename I>
 __global__ __launch_bounds__(256) void rope_kv_write_vec(RopeArgs a) {
   constexpr int kE = Lanes<E>::kPer16;
   typedef E vecE __attribute__((ext_vector_type(kE)));
   const int half = a.head_dim / 2;
   const int pairs = half / kE;  // chunk pairs per head row
   const int heads = a.num_heads + 2 * a.num_kv_heads;
-  const int64_t per_token = (int64_t)heads * pairs;
-  const int64_t total = a.n * per_token;
-  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t i = w / per_token;
+  const I per_token = (I)heads * pairs;
+  const I total = (I)a.n * per_token;
+  const I tokens = (I)a.tokens;
+  for (I w = (I)blockIdx.x * blockDim.x + threadIdx.x; w < total; w += (I)gridDim.x * blockDim.x) {
+    const I i = w / per_token;
     const int rem = (int)(w - i * per_token);
     const int hh = rem / pairs;
     const int d0 = (rem - hh * pairs) * kE;
-    const int64_t b = i / a.tokens, t = i - b * a.tokens;
+    const int64_t b = i / tokens, t = i - (I)b * tokens;
     if (hh >= a.num_heads + a.num_kv_heads) {  // v: copy both halves
       const int h = hh - a.num_heads - a.num_kv_heads;
       const int64_t slot = a.slots[i];
@@ -268,9 +271,16 @@ extern "C" int li_rope_kv_write(const void* q, const int64_t* q_strides, const v
   if (vec_ok(a, esize)) {
     const int64_t work = n * heads * (head_dim / 2 / (16 / esize));
     const int64_t blocks = std::min<int64_t>(li::cdiv64(work, threads), 65536);
-    if (dtype == LI_F32) hipLaunchKernelGGL(rope_kv_write_vec<float>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
-    else if (dtype == LI_BF16) hipLaunchKernelGGL(rope_kv_write_vec<li_bf16>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
-    else hipLaunchKernelGGL(rope_kv_write_vec<li_f16>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
+    const dim3 grid((unsigned)blocks), block(threads);
+    if (work < (int64_t)1 << 31) {
+      if (dtype == LI_F32) hipLaunchKernelGGL((rope_kv_write_vec<float, uint32_t>), grid, block, 0, s, a);
+      else if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, uint32_t>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, uint32_t>), grid, block, 0, s, a);
+    } else {
+      if (dtype == LI_F32) hipLaunchKernelGGL((rope_kv_write_vec<float, int64_t>), grid, block, 0, s, a);
+      else if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, int64_t>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, int64_t>), grid, block, 0, s, a);
+    }
   } else {
     const int64_t work = n * heads * (head_dim / 2);
     const int64_t blocks = std::min<int64_t>(li::cdiv64(work, threads), 65536);
