@@ -1,0 +1,111 @@
+"""A decode step captured into a HIP graph replays correctly for changing contexts.
+
+The reference captures its decode steps (liteinfer/engine/cuda_graphs.py:
+105-260): the slot table and context lengths are static buffers rewritten
+before each replay, columns past a row's context hold stale slots, and the
+kernels' grids may depend on host integers only. This captures the fused RoPE
++ slot-write and the paged decode of one layer, then replays it with new
+contexts, queries and slot tables, checking every replay against the same
+calls run eagerly, with eager work and synchronisations between replays.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from liteinfer_amd.paged_kernels import paged_decode
+from liteinfer_amd.rope import rope_kv_write
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+
+
+class _Step:
+    def __init__(self, batch=16, width=2048, heads=32, kv_heads=8, dim=128, num_slots=1 << 16, seed=0):
+        self.g = torch.Generator(device=DEV).manual_seed(seed)
+        self.batch, self.width, self.heads, self.kv_heads, self.dim = batch, width, heads, kv_heads, dim
+        self.num_slots = num_slots
+        bf = torch.bfloat16
+        self.key_pool = torch.randn(num_slots, kv_heads, dim, generator=self.g, device=DEV).to(bf)
+        self.value_pool = torch.randn(num_slots, kv_heads, dim, generator=self.g, device=DEV).to(bf)
+        # static inputs of the captured step
+        self.q = torch.empty(batch, 1, heads, dim, dtype=bf, device=DEV)
+        self.k = torch.empty(batch, 1, kv_heads, dim, dtype=bf, device=DEV)
+        self.v = torch.empty_like(self.k)
+        self.cos = torch.empty(batch, 1, dim, dtype=bf, device=DEV)
+        self.sin = torch.empty_like(self.cos)
+        self.slot_table = torch.empty(batch, width, dtype=torch.int64, device=DEV)
+        self.context_lens = torch.empty(batch, dtype=torch.int32, device=DEV)
+        self.write_slots = torch.empty(1, batch, dtype=torch.int64, device=DEV)
+
+    def refill(self, seed):
+        """New contexts, tables (stale columns past each context), projections and angles."""
+        g = torch.Generator(device=DEV).manual_seed(1000 + seed)
+        ctx = torch.randint(1, self.width + 1, (self.batch,), generator=g, device=DEV, dtype=torch.int32)
+        table = torch.randint(0, self.num_slots, (self.batch, self.width), generator=g, device=DEV)
+        self.context_lens.copy_(ctx)
+        self.slot_table.copy_(table)
+        self.write_slots.copy_(table.gather(1, (ctx.long() - 1)[:, None]).view(1, -1))
+        for t in (self.q, self.k, self.v):
+            t.copy_(torch.randn(t.shape, generator=g, device=DEV).to(t.dtype))
+        ang = torch.rand(self.batch, 1, self.dim // 2, generator=g, device=DEV) * 6.28
+        emb = torch.cat((ang, ang), dim=-1)
+        self.cos.copy_(emb.cos().to(self.cos.dtype))
+        self.sin.copy_(emb.sin().to(self.sin.dtype))
+
+    def run(self):
+        q = rope_kv_write(self.q.transpose(1, 2), self.k.transpose(1, 2), self.v.transpose(1, 2), self.cos, self.sin,
+                          self.write_slots, self.key_pool, self.value_pool)
+        return paged_decode(q.squeeze(2), self.key_pool, self.value_pool, self.slot_table, self.context_lens,
+                            self.dim ** -0.5, self.heads // self.kv_heads)
+
+
+def test_captured_decode_step_matches_eager_on_every_replay():
+    step = _Step()
+    step.refill(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step.run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step.run()
+    for r in range(1, 6):
+        step.refill(r)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = step.run()  # the same inputs: the slot-write rewrites identical rows
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), f"replay {r} differs from the eager step"
+        # unrelated eager work between replays
+        torch.randn(1024, 1024, device=DEV).sum().item()
+
+
+def test_captured_grid_does_not_depend_on_contexts():
+    """Replays cover contexts from 1 key to the full table width with one capture."""
+    step = _Step(batch=8, width=4096, seed=1)
+    step.refill(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step.run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step.run()
+    for lens in ([1] * 8, [4096] * 8, [1, 4096, 33, 2048, 7, 100, 4095, 64]):
+        step.refill(len(lens) + sum(lens))
+        step.context_lens.copy_(torch.tensor(lens, dtype=torch.int32))
+        step.write_slots.copy_(step.slot_table.gather(1, (step.context_lens.long() - 1)[:, None]).view(1, -1))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = step.run()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager)
+        assert np.isfinite(replayed.float().cpu().numpy()).all()
