@@ -15,7 +15,9 @@ events on the stream they run on) against MI355X's 8 TB/s. Config 3's packed
 prefill (TFLOP/s of visible causal pairs) and config 4's long-context decode
 are reported beside it, and so is the fused RoPE + slot-write at config 3's
 packed pass and config 2's decode step, with the reference's separate torch
-ops timed on the same inputs. `cpu_baseline` times the dense eager attention
+ops timed on the same inputs, and config 5: `LLM.generate` of 256 requests x
+256 greedy tokens over a random-initialised Llama-3-8B-architecture model
+(output tokens per second, liteinfer_amd/engine/e2e.py). `cpu_baseline` times the dense eager attention
 (oracle/baseline.py) in fp32 on this host's cores over a bounded sample of the
 same step.
 
@@ -228,6 +230,7 @@ def main() -> int:
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true", help="skip configs 3 and 4")
+    parser.add_argument("--no-e2e", action="store_true", help="skip config 5 (end-to-end generate)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="first run three 1 GiB device-to-device copies (a reference kernel of known "
                              "size for rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
@@ -334,6 +337,12 @@ def main() -> int:
         result["secondary"] = secondary
         torch.cuda.empty_cache()
         step = None
+
+    if not args.no_secondary and not args.no_e2e:
+        from liteinfer_amd.engine import e2e
+
+        result.setdefault("secondary", {})["e2e_c5"] = e2e.run(seed=args.seed)
+        torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
         sample_step = decode_step("c2", seed=args.seed)

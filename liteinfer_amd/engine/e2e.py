@@ -1,0 +1,66 @@
+"""The end-to-end configuration: `LLM.generate` over a random-initialised
+Llama-3-8B-architecture model with the HIP `paged` attention.
+
+256 requests of random token ids, prompt lengths lognormal with median 512
+(sigma 0.7) clipped to [16, 4096], 256 greedy output tokens each (fixed
+length: no EOS), continuous batching over at most 256 sequences with chunked
+prefill under a token budget. The timed region is one `generate` call; model
+initialisation and the capture of every decode graph width come before it.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from liteinfer_amd.engine.llm import LLM, EngineConfig
+from liteinfer_amd.engine.model import LLAMA_3_8B, RandomLlama
+
+NUM_REQUESTS = 256
+OUTPUT_TOKENS = 256
+PROMPT_MEDIAN = 512
+PROMPT_SIGMA = 0.7
+PROMPT_CLIP = (16, 4096)
+
+
+def prompts(seed: int = 0, n: int = NUM_REQUESTS, vocab: int = LLAMA_3_8B.vocab_size) -> list[list[int]]:
+    rng = np.random.default_rng(seed)
+    lens = np.clip(np.round(rng.lognormal(math.log(PROMPT_MEDIAN), PROMPT_SIGMA, size=n)), *PROMPT_CLIP).astype(int)
+    return [rng.integers(0, vocab, size=int(m)).tolist() for m in lens]
+
+
+def run(seed: int = 0, config: EngineConfig | None = None, num_requests: int = NUM_REQUESTS,
+        output_tokens: int = OUTPUT_TOKENS) -> dict:
+    config = config or EngineConfig(max_num_seqs=256, max_model_len=PROMPT_CLIP[1] + OUTPUT_TOKENS,
+                                    max_num_batched_tokens=8192, num_gpu_blocks=32768)
+    model = RandomLlama(LLAMA_3_8B, seed=seed)
+    llm = LLM(model, config)
+    # warm-up: kernels, allocator, and every decode graph width
+    llm.generate(prompts(seed + 1, n=8), max_tokens=4)
+    if llm.runner.graphs is not None:
+        llm.runner.graphs.capture_all()
+    reqs = prompts(seed, n=num_requests)
+    _, stats = llm.generate(reqs, max_tokens=output_tokens)
+    return {
+        "output_tok_per_s": round(stats.output_tokens_per_s, 1),
+        "total_tok_per_s": round((stats.output_tokens + stats.prompt_tokens) / stats.wall_s, 1),
+        "wall_s": round(stats.wall_s, 3),
+        "requests": num_requests,
+        "prompt_tokens": stats.prompt_tokens,
+        "output_tokens": stats.output_tokens,
+        "steps": stats.steps,
+        "decode_steps": stats.decode_steps,
+        "model": "Llama-3-8B architecture, random init (std 0.02), bf16",
+        "max_num_seqs": config.max_num_seqs,
+        "max_num_batched_tokens": config.max_num_batched_tokens,
+        "decode_graphs": config.use_graphs,
+        "parameter_bytes": model.parameter_bytes(),
+    }
+
+
+if __name__ == "__main__":
+    import json
+
+    print(json.dumps(run()))

@@ -1,0 +1,89 @@
+"""The generate loop (liteinfer/llm.py `LLM.generate` over the engine core), greedy
+and token-id only: each step schedules, runs one forward, samples the argmax
+for every sequence whose prompt is complete, and retires sequences that reached
+their `max_tokens` (stop strings and EOS do not apply: the end-to-end
+configuration fixes every output at its length).
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass
+
+import torch
+
+from liteinfer_amd.cache.block_pool import BlockPool
+from liteinfer_amd.cache.kv_cache import KVCache
+from liteinfer_amd.engine.model import RandomLlama
+from liteinfer_amd.engine.runner import ModelRunner
+from liteinfer_amd.engine.scheduler import Scheduler, Sequence, SequenceStatus
+
+
+@dataclass
+class EngineConfig:
+    max_num_seqs: int = 256
+    max_model_len: int = 4352
+    max_num_batched_tokens: int = 8192
+    num_gpu_blocks: int = 24576
+    block_size: int = 16
+    use_graphs: bool = True
+
+
+@dataclass
+class GenerateStats:
+    wall_s: float
+    steps: int
+    decode_steps: int
+    prompt_tokens: int
+    output_tokens: int
+
+    @property
+    def output_tokens_per_s(self) -> float:
+        return self.output_tokens / self.wall_s
+
+
+class LLM:
+    def __init__(self, model: RandomLlama, config: EngineConfig = EngineConfig()) -> None:
+        s = model.shape
+        self.config = config
+        self.model = model
+        pool = BlockPool(num_blocks=config.num_gpu_blocks, block_size=config.block_size, num_layers=s.num_layers,
+                         num_kv_heads=s.num_kv_heads, head_dim=s.head_dim, dtype=model.dtype, device=model.device)
+        self.cache = KVCache(pool)
+        self.runner = ModelRunner(model, self.cache, config.max_num_seqs, config.max_model_len, config.use_graphs)
+        self.scheduler = Scheduler(config.max_num_seqs, config.max_num_batched_tokens)
+
+    def generate(self, prompts: list[list[int]], max_tokens: int) -> tuple[list[list[int]], GenerateStats]:
+        """Greedy continuation of every prompt to exactly `max_tokens` tokens."""
+        seqs = []
+        for i, p in enumerate(prompts):
+            if len(p) + max_tokens > self.config.max_model_len:
+                raise ValueError(f"request {i}: {len(p)} + {max_tokens} tokens exceed max_model_len")
+            seq = Sequence(f"req-{i}", list(p), max_tokens)
+            seqs.append(seq)
+            self.scheduler.add(seq)
+        steps = decode_steps = 0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while self.scheduler.has_unfinished():
+            out = self.scheduler.schedule()
+            counts = [out.num_scheduled_tokens[s.request_id] for s in out.seqs]
+            logits = self.runner.execute(out.seqs, counts)
+            steps += 1
+            decode_steps += all(c == 1 for c in counts)
+            sample = [i for i, s in enumerate(out.seqs) if s.num_computed_tokens == len(s)]
+            if sample:
+                rows = torch.tensor(sample, device=logits.device)
+                tokens = logits.index_select(0, rows).argmax(dim=-1).tolist()
+                for i, tok in zip(sample, tokens):
+                    seq = out.seqs[i]
+                    seq.output_token_ids.append(int(tok))
+                    if len(seq.output_token_ids) >= seq.max_tokens:
+                        seq.status = SequenceStatus.FINISHED_LENGTH
+            for seq in self.scheduler.remove_finished():
+                self.runner.release(seq)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        stats = GenerateStats(wall, steps, decode_steps, sum(len(p) for p in prompts),
+                              sum(len(s.output_token_ids) for s in seqs))
+        return [s.output_token_ids for s in seqs], stats

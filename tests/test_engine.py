@@ -1,0 +1,58 @@
+"""The engine's scheduler: the reference's token-budget rules (liteinfer/engine/scheduler.py)."""
+
+import pytest
+
+from liteinfer_amd.engine.scheduler import Scheduler, Sequence, SequenceStatus
+
+
+def _seq(rid, prompt_len, max_tokens=4):
+    return Sequence(rid, list(range(prompt_len)), max_tokens)
+
+
+def test_prompts_are_granted_until_the_budget_runs_out_and_the_last_one_is_chunked():
+    s = Scheduler(max_num_seqs=8, token_budget=100)
+    for rid, n in (("a", 30), ("b", 50), ("c", 40)):
+        s.add(_seq(rid, n))
+    out = s.schedule()
+    assert [q.request_id for q in out.seqs] == ["a", "b", "c"]
+    assert out.num_scheduled_tokens == {"a": 30, "b": 50, "c": 20}
+
+
+def test_running_sequences_are_served_before_waiting_ones():
+    s = Scheduler(max_num_seqs=8, token_budget=10)
+    a, b = _seq("a", 4), _seq("b", 20)
+    s.add(a)
+    s.add(b)
+    out = s.schedule()
+    assert out.num_scheduled_tokens == {"a": 4, "b": 6}
+    a.num_computed_tokens, b.num_computed_tokens = 4, 6
+    a.output_token_ids.append(7)  # a decodes next
+    out = s.schedule()
+    assert [q.request_id for q in out.seqs] == ["a", "b"]
+    assert out.num_scheduled_tokens == {"a": 1, "b": 9}
+
+
+def test_max_num_seqs_caps_admission():
+    s = Scheduler(max_num_seqs=2, token_budget=1000)
+    for i in range(5):
+        s.add(_seq(f"r{i}", 3))
+    out = s.schedule()
+    assert len(out.seqs) == 2 and len(s.waiting) == 3
+
+
+def test_finished_sequences_leave_and_free_their_slot():
+    s = Scheduler(max_num_seqs=1, token_budget=16)
+    a, b = _seq("a", 2), _seq("b", 2)
+    s.add(a)
+    s.add(b)
+    s.schedule()
+    a.status = SequenceStatus.FINISHED_LENGTH
+    assert s.remove_finished() == [a]
+    out = s.schedule()
+    assert [q.request_id for q in out.seqs] == ["b"]
+    assert s.has_unfinished()
+
+
+def test_nonsense_configuration_is_refused():
+    with pytest.raises(ValueError):
+        Scheduler(max_num_seqs=0, token_budget=8)
