@@ -46,6 +46,8 @@ struct TileLayout {
   static constexpr int kInsts = 32 / kRowsPerInst;
   static constexpr int kRowBytes = D * 2;
   static constexpr int kTileBytes = 2 * 32 * kRowBytes;  // K then V
+  // Key k + 16 sits this many bytes below key k (same swizzle: kCh divides 16).
+  static constexpr int kRow16 = (16 / kInsts) * kRowBytes;
   __device__ static int row_of(int key) { return kRowsPerInst * (key % kInsts) + key / kInsts; }
   __device__ static int offset(int key, int chunk) {  // byte offset within the K (or V) half
     return row_of(key) * kRowBytes + 16 * (chunk ^ (key % kCh));
@@ -142,6 +144,23 @@ __device__ __forceinline__ Frag li_read_vt(const char* vtile, int blk, int lane)
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(p);
+}
+
+// 16-byte LDS read at LDS byte address `addr` (an address plus a constant
+// folds into the instruction's immediate offset).
+template <typename Frag>
+__device__ __forceinline__ Frag lds_read_frag(uint32_t addr) {
+  return *(const __attribute__((address_space(3))) Frag*)(uintptr_t)addr;
+}
+
+// li_read_vt from precomputed LDS byte addresses of its two transposing reads.
+template <typename Frag>
+__device__ __forceinline__ Frag lds_read_vt(uint32_t lo, uint32_t hi) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(uintptr_t)lo);
+  const v4s y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(uintptr_t)hi);
+  const short __attribute__((ext_vector_type(8))) xy = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+  return __builtin_bit_cast(Frag, xy);
 }
 
 constexpr float kLog2eMfma = 1.4426950408889634f;

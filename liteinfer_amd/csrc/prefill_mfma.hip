@@ -40,6 +40,8 @@
 #include "li_attention.h"
 #include "li_mfma.h"
 
+#include <type_traits>
+
 namespace li {
 namespace {
 
@@ -157,63 +159,93 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int i = 0; i < D / 16 + 1; ++i) acc[nb][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   const Frag ones = li_ones<Frag>();
 
-  // Folds the 32 keys of `tile` whose first key is t0 into both row blocks.
-  auto fold = [&](const char* tile, int t0) __attribute__((always_inline)) {
-    const char* vtile = tile + 32 * L::kRowBytes;
-    // S^T, one 16-key block at a time so only its K operands are live.
-    floatx4_t s[2][2];
-    // Raised priority while this wave issues MFMAs, so the SIMD's other
-    // wave's vector work fills in around them rather than the reverse.
+  // Per-lane LDS byte offsets within a 32-key tile, fixed for the whole
+  // kernel; a tile's and a stage's base are compile-time constants below, so
+  // every LDS read is one instruction with an immediate offset.
+  //   K operand of key block b (keys 16b..16b+15 of a tile), step j: key n,
+  //   chunk 4j + g. Key 16 + n sits L::kRow16 bytes below key n with the
+  //   same swizzle, so b only adds an immediate.
+  //   V^T operand of dims 16 blk..: li_read_vt's two addresses, the second
+  //   again L::kRow16 bytes below the first.
+  uint32_t koff[kSteps], voff[D / 16];
+  {
+    const uint32_t base = lds_addr(&stages[0][0]);
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) koff[j] = base + L::offset(n, 4 * j + g);
+    const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
+#pragma unroll
+    for (int blk = 0; blk < D / 16; ++blk) voff[blk] = base + L::offset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
+  }
+
+  // Folds the 64 keys of stage S (first key t0) into both row blocks: scores
+  // of all 64 keys, one softmax update per row block, then P V.
+  auto fold = [&](auto stage_tag, int t0) __attribute__((always_inline)) {
+    constexpr int S = decltype(stage_tag)::value;
+    constexpr uint32_t kStage = S * 2 * L::kTileBytes;
+    constexpr uint32_t kRow16 = L::kRow16;
+    // s[nb][b]: lane (n, g) holds the scores of keys 16 b + 4 g + r, r < 4,
+    // of row n of block nb.
+    floatx4_t s[2][4];
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t tb = kStage + (b >> 1) * L::kTileBytes + (b & 1) * kRow16;
       Frag kf[kSteps];
 #pragma unroll
-      for (int j = 0; j < kSteps; ++j) kf[j] = *reinterpret_cast<const Frag*>(tile + L::offset(16 * b + n, 4 * j + g));
+      for (int j = 0; j < kSteps; ++j) kf[j] = lds_read_frag<Frag>(koff[j] + tb);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        s[nb][b] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+        s[nb][b] = M::mma(kf[0], qf[nb][0], floatx4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int j = 0; j < kSteps; ++j) s[nb][b] = M::mma(kf[j], qf[nb][j], s[nb][b]);
+        for (int j = 1; j < kSteps; ++j) s[nb][b] = M::mma(kf[j], qf[nb][j], s[nb][b]);
       }
-      __builtin_amdgcn_sched_barrier(0);
     }
     __builtin_amdgcn_s_setprio(0);
-    // Online softmax per row block; the scale is folded into the exponent.
-    Frag pf[2];
+    // Online softmax per row block over the stage's 64 keys; the scale is
+    // folded into the exponent.
+    Frag pf[2][2];
     float alpha[2];
     bool rescale = false;
+    const bool masked = t0 + kStageKeys - 1 > lim_lo;  // reaches past some row's last key
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      float x[8];
+      if (masked) {
+        // Key t0 + 16 b + 4 g + r is visible iff 16 b + r <= lim - t0 - 4 g.
+        const int d = lim[nb] - t0 - 4 * g;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = s[nb][0][r];
-        x[4 + r] = s[nb][1][r];
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[nb][b][r] = (16 * b + r <= d) ? s[nb][b][r] : -INFINITY;
       }
-      if (t0 + 31 > lim_lo) {  // the tile reaches past some row's last key
+      float mx = fmaxf(fmaxf(s[nb][0][0], s[nb][0][1]), s[nb][0][2]);
+      mx = fmaxf(fmaxf(mx, s[nb][0][3]), s[nb][1][0]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = (t0 + kappa(g, e) <= lim[nb]) ? x[e] : -INFINITY;
+      for (int b = 1; b < 4; ++b) {
+        if (b > 1) mx = fmaxf(fmaxf(mx, s[nb][b][0]), s[nb][b][1]);
+        else mx = fmaxf(mx, s[nb][b][1]);
+        mx = fmaxf(fmaxf(mx, s[nb][b][2]), s[nb][b][3]);
       }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x[e]);
-      mx = li_group_max(mx);
-      mx *= sc;
-      // Lazy rescale: the running maximum only moves when a tile beats it by
-      // more than kLazyRescale (log2 units), so most tiles leave the
+      mx = li_group_max(mx) * sc;
+      // Lazy rescale: the running maximum only moves when the stage beats it
+      // by more than kLazyRescale (log2 units), so most stages leave the
       // accumulator alone; the weights are then at most 2^kLazyRescale.
       const float mnew = (mx > m[nb] + kLazyRescale) ? mx : m[nb];
-      alpha[nb] = __builtin_amdgcn_exp2f(m[nb] - mnew);
       rescale |= mnew != m[nb];
-      float p[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
+      alpha[nb] = __builtin_amdgcn_exp2f(m[nb] - mnew);
       m[nb] = mnew;
-      u32x4_t pw;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
-      pf[nb] = __builtin_bit_cast(Frag, pw);
+      for (int t = 0; t < 2; ++t) {
+        float p[8];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          p[r] = __builtin_amdgcn_exp2f(fmaf(s[nb][2 * t][r], sc, -mnew));
+          p[4 + r] = __builtin_amdgcn_exp2f(fmaf(s[nb][2 * t + 1][r], sc, -mnew));
+        }
+        u32x4_t pw;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
+        pf[nb][t] = __builtin_bit_cast(Frag, pw);
+      }
     }
     if (__any(rescale)) {
 #pragma unroll
@@ -223,22 +255,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[nb][i][r] *= alpha[nb];
     }
-    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
-    // O^T += V^T P^T, 16 dims at a time. The V^T operand comes straight out
-    // of LDS through transposing reads (li_read_vt): lane (m, g) gets dim
-    // 16 blk + m of keys kappa(g, 0..7).
+    // O^T += V^T P^T, 16 dims at a time, for each 32-key tile of the stage.
 #pragma unroll
-    for (int blk = 0; blk < D / 16; ++blk) {
-      const Frag vf = li_read_vt<L, Frag>(vtile, blk, lane);
+    for (int t = 0; t < 2; ++t) {
+      constexpr uint32_t kV = 32 * L::kRowBytes;
+      const uint32_t tb = kStage + t * L::kTileBytes + kV;
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf, pf[nb], acc[nb][blk]);
+      for (int blk = 0; blk < D / 16; ++blk) {
+        const Frag vf = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + kRow16);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf, pf[nb][t], acc[nb][blk]);
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acc[nb][D / 16] = M::mma(ones, pf[nb][t], acc[nb][D / 16]);
     }
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) acc[nb][D / 16] = M::mma(ones, pf[nb], acc[nb][D / 16]);
     __builtin_amdgcn_s_setprio(0);
   };
 
+  using Stage0 = std::integral_constant<int, 0>;
+  using Stage1 = std::integral_constant<int, 1>;
   for (int c0 = 0; c0 < kend; c0 += kSlotChunk) {
     const int c1 = min(c0 + kSlotChunk, kend);
     const int ntiles = (c1 - c0 + kStageKeys - 1) / kStageKeys;
@@ -250,17 +286,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
     // Two stages: the next 64 keys land in one while the other is folded.
     // Past the chunk the look-ahead re-reads a real stage (cache hits), so
-    // every wave has the same loads in flight at every wait.
+    // every wave has the same loads in flight at every wait. The loop body
+    // handles both stages so that each stage's LDS offsets are constants.
     issue_stage<T, D>(stages[0], kpool, vpool, sl, row_bytes, 0, lane, w);
-    for (int ti = 0; ti < ntiles; ++ti) {
-      issue_stage<T, D>(stages[(ti + 1) & 1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kSlotChunk),
-                        lane, w);
+    for (int ti = 0; ti < ntiles; ti += 2) {
+      issue_stage<T, D>(stages[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kSlotChunk), lane, w);
       li_wait_vm<kDmaPerStage>();
       __syncthreads();
-      const char* stage = stages[ti & 1];
-      fold(stage, c0 + kStageKeys * ti);
-      __builtin_amdgcn_sched_barrier(0);  // one 32-key fold's registers at a time
-      fold(stage + L::kTileBytes, c0 + kStageKeys * ti + 32);
+      fold(Stage0{}, c0 + kStageKeys * ti);
+      __syncthreads();
+      if (ti + 1 >= ntiles) break;
+      issue_stage<T, D>(stages[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kSlotChunk), lane, w);
+      li_wait_vm<kDmaPerStage>();
+      __syncthreads();
+      fold(Stage1{}, c0 + kStageKeys * (ti + 1));
       __syncthreads();
     }
     li_wait_vm<0>();
