@@ -45,49 +45,66 @@
 namespace li {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kRows = 128;  // (query, head) rows per work-group
+// A work-group has W waves and 32 W (query, head) rows. Eight waves (two per
+// SIMD) share each K/V stage: half the LDS fill per MFMA of four.
+constexpr int kWaves = 8;
+constexpr int kMinRows = 32 * kWaves;  // rows of a work-group
 constexpr int kStageKeys = 64;
 
+// V tiles use their own chunk swizzle: chunk c of key k sits in slot
+// c ^ vswizzle(k). A transposing V^T read (li_read_vt's addressing) has each
+// group of 16 lanes read chunks 2 blk and 2 blk + 1 of four consecutive keys
+// k (and 32 lanes eight keys); with vswizzle(k) = 2 (k mod CH / 2) those land
+// in slots 2 (blk ^ (k mod CH / 2)) + {0, 1}, all distinct, so the reads hit
+// distinct banks (the K swizzle would map pairs of them onto one slot). Keys
+// k and k + 16 share a swizzle, like the K layout's.
+template <int D>
+__device__ __forceinline__ int vswizzle(int key) {
+  return 2 * (key % (D / 16));
+}
+
 // Issues this wave's share of the direct-to-LDS loads of the 64 keys whose
-// first key is entry `t` of the staged slots: of each 32-key half, the
-// instructions i = w * kInsts / 4 + ... (K and V).
-template <typename T, int D>
+// first key is entry `t` of the staged slots. The stage takes 2 * kInsts
+// instructions each for K and V (kInsts per 32-key half); wave w issues
+// pairs p = w * kPer .. w * kPer + kPer - 1, pair p being instruction
+// p % kInsts of half p / kInsts.
+template <typename T, int D, int W>
 __device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ kpool, const T* __restrict__ vpool,
                                             const int* __restrict__ sl, uint32_t row_bytes, int t, int lane, int w) {
   using L = TileLayout<D>;
-  constexpr int kPerWave = L::kInsts / kWaves;
+  constexpr int kPer = 2 * L::kInsts / W;
+  static_assert(kPer >= 1 && kPer * W == 2 * L::kInsts, "waves must split the stage's loads evenly");
   const int rr = lane / L::kCh, nn = lane % L::kCh;
   // All slot reads first: each load below is an asm statement with a memory
   // clobber, so a read placed after one would wait for its own round trip.
-  uint32_t slot[2][kPerWave];
+  uint32_t slot[kPer];
 #pragma unroll
-  for (int half = 0; half < 2; ++half)
+  for (int ii = 0; ii < kPer; ++ii) {
+    const int p = w * kPer + ii, half = p / L::kInsts, i = p % L::kInsts;
+    slot[ii] = (uint32_t)sl[t + 32 * half + rr * L::kInsts + i];
+  }
 #pragma unroll
-    for (int ii = 0; ii < kPerWave; ++ii) slot[half][ii] = (uint32_t)sl[t + 32 * half + rr * L::kInsts + w * kPerWave + ii];
-#pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    char* tile = stage + half * L::kTileBytes;
-#pragma unroll
-    for (int ii = 0; ii < kPerWave; ++ii) {
-      const int i = w * kPerWave + ii;
-      const int key = rr * L::kInsts + i;
-      const int chunk = nn ^ (key % L::kCh);
-      const uint32_t dst = lds_addr(tile + i * 1024);
-      dma16(row_ptr(kpool + 8 * chunk, slot[half][ii], row_bytes), dst);
-      dma16(row_ptr(vpool + 8 * chunk, slot[half][ii], row_bytes), dst + 32 * L::kRowBytes);
-    }
+  for (int ii = 0; ii < kPer; ++ii) {
+    const int p = w * kPer + ii, half = p / L::kInsts, i = p % L::kInsts;
+    const int key = rr * L::kInsts + i;
+    const uint32_t dst = lds_addr(stage + half * L::kTileBytes + i * 1024);
+    // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
+    dma16(row_ptr(kpool + 8 * (nn ^ (key % L::kCh)), slot[ii], row_bytes), dst);
+    dma16(row_ptr(vpool + 8 * (nn ^ vswizzle<D>(key)), slot[ii], row_bytes), dst + 32 * L::kRowBytes);
   }
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma(AttnArgs a) {
+template <typename T, int D, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma(AttnArgs a) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
   using L = TileLayout<D>;
   constexpr int kSteps = D / 32;
-  constexpr int kDmaPerStage = 2 * 2 * (L::kInsts / kWaves);
-  __shared__ __attribute__((aligned(16))) int sl[kSlotChunk + kStageKeys];
+  constexpr int kDmaPerStage = 2 * (2 * L::kInsts / W);
+  // Keys whose slots are staged in LDS at a time (restaging costs a pipeline
+  // drain, so chunks are long).
+  constexpr int kChunk = 4096;
+  __shared__ __attribute__((aligned(16))) int sl[kChunk + kStageKeys];
   __shared__ __attribute__((aligned(1024))) char stages[2][2 * L::kTileBytes];
 
   const int tid = threadIdx.x;
@@ -103,7 +120,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   const int first_tok = a.qsl[seq];
   const int nq = a.qsl[seq + 1] - first_tok;
-  const int bq = a.block_q;  // query tokens per block = kRows / groups
+  const int bq = a.block_q;  // query tokens per block = 32 W / groups
   const int q0 = qblock * bq;
   if (q0 >= nq) return;
   if (nq == 1 && a.single_query_elsewhere) return;  // the decode kernel serves it
@@ -141,6 +158,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int lim[2] = {min(pos[0], kend - 1), min(pos[1], kend - 1)};
   // Below the block's first query position every row sees every key.
   const int lim_lo = min(pos0 + q0, kend - 1);
+  // A wave whose 32 rows are all padding (a sequence's last, partial block)
+  // only helps load the stages; it folds nothing, leaving its SIMD to the
+  // other wave there.
+  const bool idle = 32 * w >= (q1 - q0) * G;
 
   const T* kpool = static_cast<const T*>(a.kp) + (int64_t)kvh * a.p_s1;
   const T* vpool = static_cast<const T*>(a.vp) + (int64_t)kvh * a.p_s1;
@@ -165,8 +186,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   //   K operand of key block b (keys 16b..16b+15 of a tile), step j: key n,
   //   chunk 4j + g. Key 16 + n sits L::kRow16 bytes below key n with the
   //   same swizzle, so b only adds an immediate.
-  //   V^T operand of dims 16 blk..: li_read_vt's two addresses, the second
-  //   again L::kRow16 bytes below the first.
+  //   V^T operand of dims 16 blk..: li_read_vt's two addresses (with the V
+  //   swizzle), the second again L::kRow16 bytes below the first.
   uint32_t koff[kSteps], voff[D / 16];
   {
     const uint32_t base = lds_addr(&stages[0][0]);
@@ -174,7 +195,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     for (int j = 0; j < kSteps; ++j) koff[j] = base + L::offset(n, 4 * j + g);
     const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
 #pragma unroll
-    for (int blk = 0; blk < D / 16; ++blk) voff[blk] = base + L::offset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
+    for (int blk = 0; blk < D / 16; ++blk)
+      voff[blk] = base + L::row_of(key) * L::kRowBytes + 16 * ((2 * blk + (a4 >> 1)) ^ vswizzle<D>(key)) + 8 * (a4 & 1);
   }
 
   // Folds the 64 keys of stage S (first key t0) into both row blocks: scores
@@ -275,31 +297,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   using Stage0 = std::integral_constant<int, 0>;
   using Stage1 = std::integral_constant<int, 1>;
-  for (int c0 = 0; c0 < kend; c0 += kSlotChunk) {
-    const int c1 = min(c0 + kSlotChunk, kend);
+  for (int c0 = 0; c0 < kend; c0 += kChunk) {
+    const int c1 = min(c0 + kChunk, kend);
     const int ntiles = (c1 - c0 + kStageKeys - 1) / kStageKeys;
     // Stage this chunk's slots plus one stage past its end; entries past the
     // chunk repeat its last slot so every load reads a real row.
     __syncthreads();
-    for (int i = tid; i < kSlotChunk + kStageKeys; i += 256) sl[i] = (int)srow[min(c0 + i, c1 - 1)];
+    for (int i = tid; i < kChunk + kStageKeys; i += 64 * W) sl[i] = (int)srow[min(c0 + i, c1 - 1)];
     __syncthreads();
 
     // Two stages: the next 64 keys land in one while the other is folded.
     // Past the chunk the look-ahead re-reads a real stage (cache hits), so
     // every wave has the same loads in flight at every wait. The loop body
     // handles both stages so that each stage's LDS offsets are constants.
-    issue_stage<T, D>(stages[0], kpool, vpool, sl, row_bytes, 0, lane, w);
+    issue_stage<T, D, W>(stages[0], kpool, vpool, sl, row_bytes, 0, lane, w);
     for (int ti = 0; ti < ntiles; ti += 2) {
-      issue_stage<T, D>(stages[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kSlotChunk), lane, w);
+      issue_stage<T, D, W>(stages[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
       li_wait_vm<kDmaPerStage>();
       __syncthreads();
-      fold(Stage0{}, c0 + kStageKeys * ti);
+      if (!idle) fold(Stage0{}, c0 + kStageKeys * ti);
       __syncthreads();
       if (ti + 1 >= ntiles) break;
-      issue_stage<T, D>(stages[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kSlotChunk), lane, w);
+      issue_stage<T, D, W>(stages[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
       li_wait_vm<kDmaPerStage>();
       __syncthreads();
-      fold(Stage1{}, c0 + kStageKeys * (ti + 1));
+      if (!idle) fold(Stage1{}, c0 + kStageKeys * (ti + 1));
       __syncthreads();
     }
     li_wait_vm<0>();
@@ -394,8 +416,8 @@ bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
 
 size_t prefill_work_entries(int batch, int max_context) {
   // A sequence's queries are the last of its context, so it has at most
-  // max_context of them; blocks hold at least kRows / 16 query tokens.
-  return (size_t)batch * cdiv(max(max_context, 1), kRows / 16);
+  // max_context of them; blocks hold at least kMinRows / 16 query tokens.
+  return (size_t)batch * cdiv(max(max_context, 1), kMinRows / 16);
 }
 
 bool prefill_mfma_applies(const AttnArgs& a, int dtype) {
@@ -406,9 +428,9 @@ bool prefill_mfma_applies(const AttnArgs& a, int dtype) {
          rows_aligned(a.kp, a.p_s0, a.p_s1, 2) && rows_aligned(a.vp, a.p_s0, a.p_s1, 2);
 }
 
-int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) {
-  AttnArgs a = in;
-  a.block_q = kRows / a.groups;
+template <int W>
+static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
+  a.block_q = 32 * W / a.groups;
   a.num_qblocks = cdiv(a.max_query_len, a.block_q);
   const int64_t blocks = (int64_t)a.batch * a.num_kv_heads * a.num_qblocks;
   if (blocks == 0) return LI_OK;
@@ -417,15 +439,17 @@ int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) {
     return fail(LI_EINVAL, "prefill: %d query blocks per sequence exceed the planned work list", a.num_qblocks);
   hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
   if (int rc = check_launch("prefill_order")) return rc;
-  const dim3 grid((unsigned)blocks), block(256);
+  const dim3 grid((unsigned)blocks), block(64 * W);
   if (dtype == LI_BF16) {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64>), grid, block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64, W>), grid, block, 0, s, a);
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64>), grid, block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64, W>), grid, block, 0, s, a);
   }
   return check_launch("prefill_mfma");
 }
+
+int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) { return launch_prefill_waves<kWaves>(in, dtype, s); }
 
 }  // namespace li
