@@ -7,30 +7,26 @@
 // they multiply V. One wave64 per partition, 32 keys per step, laid out for
 // v_mfma_f32_16x16x32_{bf16,f16}. Lane (n, g) = (lane % 16, lane / 16).
 //
-// Loads. Lane (n, g) loads 16 bytes (dims 8n..8n+7) of K and of V for each of
-// the 8 keys kappa(g, 0..7) = {4g..4g+3, 16+4g..16+4g+3} of the tile, so each
-// load instruction reads 4 whole 256-byte pool rows, 16 lanes per row. (A
-// layout where 16 lanes each read 64 bytes of 16 different rows measured 20%
-// less HBM bandwidth.) The next tile's loads are always in flight while the
+// Loads. A tile's K and V rows go straight from the pool into LDS
+// (global_load_lds_dwordx4, the 32-key tile layout of li_mfma.h): each load
+// instruction reads 4 whole 256-byte pool rows, 16 lanes per row. (A layout
+// where 16 lanes each read 64 bytes of 16 different rows measured 20% less
+// HBM bandwidth.) The next tile's loads are always in flight while the
 // current one is folded.
 //
-//   S^T = K Q^T     A = K (16 keys x 32 dims), B = Q^T (32 dims x 16 heads).
-//                   The A operand wants lane (m, g) to hold 8 dims of key m,
-//                   so K goes through LDS once: rows written as loaded, read
-//                   back at dims 32j + 8g (rows padded to 272 bytes, so 16
-//                   lanes reading 16 rows hit 16 distinct bank groups). The
-//                   result gives lane (n, g) the scores of keys 4g..4g+3 (and
-//                   16+4g.. from the second block) for head n.
-//   O^T += V^T P^T  A = V^T (16 rows x 32 keys), B = P^T (32 keys x 16 heads).
-//                   Lane (n, g)'s 8 weights are for keys kappa(g, 0..7) of
-//                   head n: exactly its B operand, no lane exchange. Its 8
-//                   V chunks (8 keys x dims 8n..8n+7) become 8 A operands by
-//                   a register-only 8x8 transpose: row n of instruction i is
-//                   dim 8n + i.
-//   The result gives lane (n, g) dims {8(4g+r) + i} of head n, so the
+//   S^T = K Q^T     A = K (16 keys x 32 dims) read from LDS, B = Q^T
+//                   (32 dims x 16 heads) kept in registers. Lane (n, g) gets
+//                   the scores of keys 4g..4g+3 (and 16+4g.. from the second
+//                   block) for head n.
+//   O^T += V^T P^T  B = P^T: lane (n, g)'s 8 weights are for keys
+//                   kappa(g, 0..7) of head n, exactly its B operand, no lane
+//                   exchange. A = V^T (16 dims x 32 keys) comes straight out
+//                   of LDS through transposing reads (li_read_vt's
+//                   addressing, ds_read_b64_tr_b16).
+//   The result gives lane (n, g) dims 16 blk + 4g + r of head n, so the
 //   running-max rescale is per lane (its own head) and nothing is reduced
-//   across lanes except the tile maximum (two xor shuffles) and, once at the
-//   end, the denominator.
+//   across lanes except the tile maximum (two permlane swaps) and, once at
+//   the end, the denominator.
 //
 // Heads past G are zero rows of Q^T: they score 0 and are never stored.
 // Keys past the partition's end read the last key's slot (a real row) and
@@ -64,11 +60,11 @@ __device__ __forceinline__ void issue_tile(char* stage, const T* __restrict__ kp
 #pragma unroll
   for (int i = 0; i < L::kInsts; ++i) {
     const int key = rr * L::kInsts + i;
-    const int chunk = nn ^ (key % L::kCh);
     const uint32_t dst = lds_addr(stage + i * 1024);  // rows kRowsPerInst * i ..: 1 KiB per instruction
     const uint32_t row_bytes = (uint32_t)(p_s0 * sizeof(T));
-    dma16(row_ptr(kpool + 8 * chunk, (uint32_t)keys[i], row_bytes), dst);
-    dma16(row_ptr(vpool + 8 * chunk, (uint32_t)keys[i], row_bytes), dst + 32 * L::kRowBytes);
+    // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
+    dma16(row_ptr(kpool + 8 * (nn ^ (key % L::kCh)), (uint32_t)keys[i], row_bytes), dst);
+    dma16(row_ptr(vpool + 8 * (nn ^ L::vswizzle(key)), (uint32_t)keys[i], row_bytes), dst + 32 * L::kRowBytes);
   }
 }
 
@@ -80,7 +76,8 @@ struct DecodeLds {
 };
 
 // Online-softmax state of one wave: lane (n, g) holds head n's running max
-// and (partial) denominator, and dims {8(4g+r) + i} of its accumulator.
+// and (partial) denominator, and in acc[blk][r] (blk < D / 16) dim
+// 16 blk + 4 g + r of its accumulator.
 struct DecodeState {
   float m, l;
   floatx4_t acc[8];
@@ -95,9 +92,18 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
   using Frag = typename M::Frag;
   using L = TileLayout<D>;
   constexpr int kSteps = D / 32;
-  constexpr int kChunks = D / 8;
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
+  // Per-lane LDS byte offsets within a tile: the K operand of key n, step j
+  // (key 16 + n sits L::kRow16 bytes below), and li_read_vt's V^T addresses.
+  uint32_t koff[kSteps], voff[D / 16];
+#pragma unroll
+  for (int j = 0; j < kSteps; ++j) koff[j] = L::offset(n, 4 * j + g);
+  {
+    const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
+#pragma unroll
+    for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
+  }
   const T* kpool = static_cast<const T*>(a.kp) + (int64_t)kvh * a.p_s1;
   const T* vpool = static_cast<const T*>(a.vp) + (int64_t)kvh * a.p_s1;
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
@@ -118,22 +124,13 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
       for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
     }
 
-    // Folds the tile in `stage` whose first key is t0.
-    auto fold = [&](const char* stage, int t0) {
-      const char* vstage = stage + 32 * L::kRowBytes;
+    // Folds the tile in `stage` (LDS byte address) whose first key is t0.
+    auto fold = [&](uint32_t stage, int t0) __attribute__((always_inline)) {
       floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < kSteps; ++j) {
-        const Frag k0 = *reinterpret_cast<const Frag*>(stage + L::offset(n, 4 * j + g));
-        const Frag k1 = *reinterpret_cast<const Frag*>(stage + L::offset(16 + n, 4 * j + g));
-        s0 = M::mma(k0, qf[j], s0);
-        s1 = M::mma(k1, qf[j], s1);
-      }
-      u32x4_t vr[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        vr[e] = (n < kChunks) ? *reinterpret_cast<const u32x4_t*>(vstage + L::offset(kappa(g, e), n))
-                              : u32x4_t{0u, 0u, 0u, 0u};
+        s0 = M::mma(lds_read_frag<Frag>(stage + koff[j]), qf[j], s0);
+        s1 = M::mma(lds_read_frag<Frag>(stage + koff[j] + L::kRow16), qf[j], s1);
       }
       float x[8];
 #pragma unroll
@@ -145,24 +142,21 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
 #pragma unroll
         for (int e = 0; e < 8; ++e) x[e] = (t0 + kappa(g, e) < c1) ? x[e] : -INFINITY;
       }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, x[e]);
+      float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
+      mx = fmaxf(fmaxf(mx, x[3]), x[4]);
+      mx = fmaxf(fmaxf(mx, x[5]), fmaxf(x[6], x[7]));
       mx = li_group_max(mx) * sc;
       // Lazy rescale (see kLazyRescale).
       const float mnew = (mx > st.m + kLazyRescale) ? mx : st.m;
       const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
-      float psum = 0.f;
       float p[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
-        psum += p[e];
-      }
+      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
+      const float psum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
       st.l = st.l * alpha + psum;
       if (__any(mnew != st.m)) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < D / 16; ++i)
 #pragma unroll
           for (int r = 0; r < 4; ++r) st.acc[i][r] *= alpha;
       }
@@ -171,17 +165,11 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
 #pragma unroll
       for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
       const Frag pf = __builtin_bit_cast(Frag, pw);
+      // O^T += V^T P^T, 16 dims at a time, V^T straight out of LDS.
+      const uint32_t vstage = stage + 32 * L::kRowBytes;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int w = i >> 1;
-        u32x4_t va;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint32_t lo = vr[2 * u][w], hi = vr[2 * u + 1][w];
-          va[u] = (i & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
-        }
-        st.acc[i] = M::mma(__builtin_bit_cast(Frag, va), pf, st.acc[i]);
-      }
+      for (int blk = 0; blk < D / 16; ++blk)
+        st.acc[blk] = M::mma(lds_read_vt<Frag>(vstage + voff[blk], vstage + voff[blk] + L::kRow16), pf, st.acc[blk]);
     };
 
     // Two stages: while one tile is folded the next tile's loads land in the
@@ -193,11 +181,11 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
     for (int ti = 0;;) {
       issue_tile<T, D>(lds.stage[1], kpool, vpool, lds.sl, a.p_s0, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
-      fold(lds.stage[0], c0 + 32 * ti);
+      fold(lds_addr(lds.stage[0]), c0 + 32 * ti);
       if (++ti >= ntiles) break;
       issue_tile<T, D>(lds.stage[0], kpool, vpool, lds.sl, a.p_s0, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
-      fold(lds.stage[1], c0 + 32 * ti);
+      fold(lds_addr(lds.stage[1]), c0 + 32 * ti);
       if (++ti >= ntiles) break;
     }
     // Drain the look-ahead loads before the slots (and stages) are reused.
@@ -223,39 +211,28 @@ __device__ __forceinline__ void load_query(const AttnArgs& a, int row, int kvh, 
 template <typename T, int D>
 __device__ __forceinline__ void store_state(const DecodeState& st, T* orow_head0, int64_t o_s1, float* po,
                                             float* plse, int64_t p_head_stride, int groups) {
-  constexpr int kChunks = D / 8;
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
   const float lt = li_group_sum(st.l);
   if (n >= groups) return;
   const float inv = 1.f / lt;
   if (orow_head0) {
-    T* orow = orow_head0 + (int64_t)n * o_s1;
+    T* orow = orow_head0 + (int64_t)n * o_s1 + 4 * g;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int chunk = 4 * g + r;
-      if (chunk < kChunks) {
-        u32x4_t w;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = li_pack2<T>(st.acc[2 * u][r] * inv, st.acc[2 * u + 1][r] * inv);
-        *reinterpret_cast<u32x4_t*>(orow + 8 * chunk) = w;
-      }
+    for (int blk = 0; blk < D / 16; ++blk) {
+      uint2 w;
+      w.x = li_pack2<T>(st.acc[blk][0] * inv, st.acc[blk][1] * inv);
+      w.y = li_pack2<T>(st.acc[blk][2] * inv, st.acc[blk][3] * inv);
+      *reinterpret_cast<uint2*>(orow + 16 * blk) = w;
     }
   } else {
-    float* prow = po + (int64_t)n * p_head_stride * D;
+    float* prow = po + (int64_t)n * p_head_stride * D + 4 * g;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int chunk = 4 * g + r;
-      if (chunk < kChunks) {
-        floatx4_t lo4, hi4;
+    for (int blk = 0; blk < D / 16; ++blk) {
+      floatx4_t v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          lo4[i] = st.acc[i][r] * inv;
-          hi4[i] = st.acc[4 + i][r] * inv;
-        }
-        *reinterpret_cast<floatx4_t*>(prow + 8 * chunk) = lo4;
-        *reinterpret_cast<floatx4_t*>(prow + 8 * chunk + 4) = hi4;
-      }
+      for (int r = 0; r < 4; ++r) v[r] = st.acc[blk][r] * inv;
+      *reinterpret_cast<floatx4_t*>(prow + 16 * blk) = v;
     }
     if (g == 0) plse[(int64_t)n * p_head_stride] = st.m + log2f(lt);
   }

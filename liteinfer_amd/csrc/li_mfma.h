@@ -49,8 +49,19 @@ struct TileLayout {
   // Key k + 16 sits this many bytes below key k (same swizzle: kCh divides 16).
   static constexpr int kRow16 = (16 / kInsts) * kRowBytes;
   __device__ static int row_of(int key) { return kRowsPerInst * (key % kInsts) + key / kInsts; }
-  __device__ static int offset(int key, int chunk) {  // byte offset within the K (or V) half
+  __device__ static int offset(int key, int chunk) {  // byte offset within the K half
     return row_of(key) * kRowBytes + 16 * (chunk ^ (key % kCh));
+  }
+  // V rows use their own chunk swizzle: chunk c of key k sits in slot
+  // c ^ vswizzle(k). A transposing V^T read (li_read_vt's addressing) has
+  // each group of 16 lanes read chunks 2 blk and 2 blk + 1 of four
+  // consecutive keys k (and 32 lanes eight keys); with vswizzle(k) =
+  // 2 (k mod CH / 2) those land in slots 2 (blk ^ (k mod CH / 2)) + {0, 1},
+  // all distinct, so the reads hit distinct banks (the K swizzle would map
+  // pairs of them onto one slot). Keys k and k + 16 share a swizzle.
+  __device__ static int vswizzle(int key) { return 2 * (key % (kCh / 2)); }
+  __device__ static int voffset(int key, int chunk) {  // byte offset within the V half
+    return row_of(key) * kRowBytes + 16 * (chunk ^ vswizzle(key));
   }
 };
 
@@ -134,8 +145,8 @@ __device__ __forceinline__ Frag li_read_vt(const char* vtile, int blk, int lane)
   const int a = s & 3, j = s >> 2;
   const int chunk = 2 * blk + (a >> 1);
   const int byte = 8 * (a & 1);
-  const char* lo = vtile + L::offset(4 * g + j, chunk) + byte;
-  const char* hi = vtile + L::offset(16 + 4 * g + j, chunk) + byte;
+  const char* lo = vtile + L::voffset(4 * g + j, chunk) + byte;
+  const char* hi = vtile + L::voffset(16 + 4 * g + j, chunk) + byte;
   const v4s x = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(lo));
   const v4s y = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(hi));
   const short __attribute__((ext_vector_type(8))) xy = {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};

@@ -51,18 +51,6 @@ constexpr int kWaves = 8;
 constexpr int kMinRows = 32 * kWaves;  // rows of a work-group
 constexpr int kStageKeys = 64;
 
-// V tiles use their own chunk swizzle: chunk c of key k sits in slot
-// c ^ vswizzle(k). A transposing V^T read (li_read_vt's addressing) has each
-// group of 16 lanes read chunks 2 blk and 2 blk + 1 of four consecutive keys
-// k (and 32 lanes eight keys); with vswizzle(k) = 2 (k mod CH / 2) those land
-// in slots 2 (blk ^ (k mod CH / 2)) + {0, 1}, all distinct, so the reads hit
-// distinct banks (the K swizzle would map pairs of them onto one slot). Keys
-// k and k + 16 share a swizzle, like the K layout's.
-template <int D>
-__device__ __forceinline__ int vswizzle(int key) {
-  return 2 * (key % (D / 16));
-}
-
 // Issues this wave's share of the direct-to-LDS loads of the 64 keys whose
 // first key is entry `t` of the staged slots. The stage takes 2 * kInsts
 // instructions each for K and V (kInsts per 32-key half); wave w issues
@@ -90,7 +78,7 @@ __device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ k
     const uint32_t dst = lds_addr(stage + half * L::kTileBytes + i * 1024);
     // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
     dma16(row_ptr(kpool + 8 * (nn ^ (key % L::kCh)), slot[ii], row_bytes), dst);
-    dma16(row_ptr(vpool + 8 * (nn ^ vswizzle<D>(key)), slot[ii], row_bytes), dst + 32 * L::kRowBytes);
+    dma16(row_ptr(vpool + 8 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), dst + 32 * L::kRowBytes);
   }
 }
 
@@ -186,8 +174,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   //   K operand of key block b (keys 16b..16b+15 of a tile), step j: key n,
   //   chunk 4j + g. Key 16 + n sits L::kRow16 bytes below key n with the
   //   same swizzle, so b only adds an immediate.
-  //   V^T operand of dims 16 blk..: li_read_vt's two addresses (with the V
-  //   swizzle), the second again L::kRow16 bytes below the first.
+  //   V^T operand of dims 16 blk..: li_read_vt's two addresses, the second
+  //   again L::kRow16 bytes below the first.
   uint32_t koff[kSteps], voff[D / 16];
   {
     const uint32_t base = lds_addr(&stages[0][0]);
@@ -195,8 +183,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     for (int j = 0; j < kSteps; ++j) koff[j] = base + L::offset(n, 4 * j + g);
     const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
 #pragma unroll
-    for (int blk = 0; blk < D / 16; ++blk)
-      voff[blk] = base + L::row_of(key) * L::kRowBytes + 16 * ((2 * blk + (a4 >> 1)) ^ vswizzle<D>(key)) + 8 * (a4 & 1);
+    for (int blk = 0; blk < D / 16; ++blk) voff[blk] = base + L::voffset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
   }
 
   // Folds the 64 keys of stage S (first key t0) into both row blocks: scores
