@@ -12,8 +12,9 @@ token's K and V rows for all KV heads plus its int64 slot index, the queries
 and outputs, and the slot-write's reads and writes. `roofline` rates the
 decode call (the partition kernel plus the partition combine, timed with HIP
 events on the stream they run on) against MI355X's 8 TB/s. Config 3's packed
-prefill (TFLOP/s of visible causal pairs) and config 4's long-context decode
-are reported beside it, and so is the fused RoPE + slot-write at config 3's
+prefill (TFLOP/s of visible causal pairs; also its 8 chunks alone, its 56
+one-query rows alone in GB/s, and 8 chunks of 2048 queries over 8192 cached
+keys) and config 4's long-context decode are reported beside it, and so is the fused RoPE + slot-write at config 3's
 packed pass and config 2's decode step, with the reference's separate torch
 ops timed on the same inputs, and config 5: `LLM.generate` of 256 requests x
 256 greedy tokens over a random-initialised Llama-3-8B-architecture model
@@ -43,7 +44,7 @@ sys.path.insert(0, str(ROOT))
 from liteinfer_amd import _native  # noqa: E402
 from liteinfer_amd.attention import PagedKV, paged_attention  # noqa: E402
 from liteinfer_amd.cache.kv_cache import scatter_into  # noqa: E402
-from liteinfer_amd.workloads import decode_step, packed_step  # noqa: E402
+from liteinfer_amd.workloads import c3_shapes, decode_step, packed_step  # noqa: E402
 
 METRIC = "paged-decode HBM GB/s (% of peak); prefill attn TFLOP/s; e2e output tok/s"
 HBM_PEAK_GBS = 8000.0
@@ -331,6 +332,40 @@ def main() -> int:
         }
         geo3, c3_tokens = c3.geometry, sum(c3.host_query_lens)
         del c3
+        torch.cuda.empty_cache()
+        # Config 3's two kinds of work on their own: the 8 chunks (MFMA-bound)
+        # and the 56 one-query rows (HBM-bound), each as a packed pass.
+        chunks, rows = c3_shapes(args.seed)
+        part = packed_step("custom", seed=args.seed, chunks=chunks, decode_contexts=[])
+        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 4), 3))
+        part_flops = prefill_flops(part.host_query_lens, part.host_context_lens, part.geometry)
+        secondary["prefill_c3_chunks"] = {
+            "avg_us": round(part_avg * 1e3, 2),
+            "TFLOP/s": round(part_flops / (part_avg * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(part_flops / (part_avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        }
+        del part
+        torch.cuda.empty_cache()
+        part = packed_step("custom", seed=args.seed, chunks=[], decode_contexts=rows)
+        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 4), 3))
+        part_bytes = decode_bytes(part.host_context_lens, part.geometry)
+        secondary["c3_decode_rows"] = {
+            "avg_us": round(part_avg * 1e3, 2),
+            "GB/s": round(part_bytes / (part_avg * 1e-3) / 1e9, 1),
+            "frac_hbm": round(part_bytes / (part_avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        }
+        del part
+        torch.cuda.empty_cache()
+        # Long chunks: 8 chunks of 2048 queries over 8192 cached keys.
+        part = packed_step("custom", seed=args.seed, chunks=[(2048, 8192)] * 8, decode_contexts=[])
+        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 20), 2))
+        part_flops = prefill_flops(part.host_query_lens, part.host_context_lens, part.geometry)
+        secondary["prefill_8x2048_over_8192"] = {
+            "avg_us": round(part_avg * 1e3, 2),
+            "TFLOP/s": round(part_flops / (part_avg * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(part_flops / (part_avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        }
+        del part
         torch.cuda.empty_cache()
         secondary["rope_kv_write_c3"] = _time_rope(1, c3_tokens, geo3)
         secondary["rope_kv_write_c2"] = _time_rope(64, 1, geo3)

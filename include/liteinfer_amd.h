@@ -52,12 +52,17 @@ enum li_flags {
   LI_FLAG_NONE = 0,
   LI_FLAG_FORCE_GENERIC = 1, /* run the general-shape kernel even where the
                                MFMA kernel applies (used by the parity tests) */
-  LI_FLAG_EQUAL_SPLITS = 2   /* li_paged_decode on the MFMA kernel: honour
+  LI_FLAG_EQUAL_SPLITS = 2,  /* li_paged_decode on the MFMA kernel: honour
                                num_splits >= 1 as the reference's equal-slice
                                partition count. Without it the MFMA kernel
                                takes num_splits as a scheduling hint only and
                                runs its balanced split (the same attention,
                                within fp32 rounding of the partial combine) */
+  LI_FLAG_PREFILL_ONLY = 4   /* li_paged_prefill on the MFMA path: the prefill
+                               kernel serves every sequence, one-query ones
+                               included, and the split decode kernel is not
+                               launched (for passes the caller knows have no
+                               one-query sequences; correct either way) */
 };
 
 /* Message of the last failure on this thread ("" if none). */

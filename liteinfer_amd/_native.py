@@ -20,6 +20,7 @@ LI_F32, LI_F16, LI_BF16 = 0, 1, 2
 LI_OK, LI_EINVAL, LI_EUNSUPPORTED, LI_ELAUNCH, LI_EWORKSPACE = 0, -1, -2, -3, -4
 LI_FLAG_FORCE_GENERIC = 1
 LI_FLAG_EQUAL_SPLITS = 2
+LI_FLAG_PREFILL_ONLY = 4
 
 DTYPE_CODES = {torch.float32: LI_F32, torch.float16: LI_F16, torch.bfloat16: LI_BF16}
 

@@ -175,9 +175,12 @@ def _paged_packed(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_group
     """``[1, heads, total_queries, dim]`` in, the same out; the kernel works token-first."""
     from liteinfer_amd.paged_kernels import paged_prefill
 
+    # The host lengths, when the payload carries them, say whether the pass
+    # has one-query sequences for the decode kernel to take.
+    one_query_rows = (1 in kv.host_query_lens) if kv.host_query_lens else None
     out = paged_prefill(
         query.squeeze(0).transpose(0, 1), kv.key_pool, kv.value_pool, kv.slot_table, kv.context_lens,
-        kv.query_start_loc, kv.max_query_len, scaling, num_kv_groups,
+        kv.query_start_loc, kv.max_query_len, scaling, num_kv_groups, one_query_rows=one_query_rows,
     )
     return out.transpose(0, 1).unsqueeze(0)
 

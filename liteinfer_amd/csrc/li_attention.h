@@ -42,7 +42,11 @@ struct AttnArgs {
   int single_query_elsewhere;  // prefill: one-query sequences are served by the decode kernel
   int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
   int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
+  int* queue;    // MFMA prefill: kPrefillQueues unit counters, then the number of blocks listed in `work`
 };
+
+// Work queues of the persistent MFMA prefill grid (one per XCD).
+constexpr int kPrefillQueues = 8;
 
 // Largest head_dim the general-shape kernel serves.
 constexpr int kGenericMaxHeadDim = 512;

@@ -223,10 +223,10 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
 }
 
 // Workspace of the MFMA prefill path: the balanced decode kernel's partials
-// for the one-query sequences, then the prefill work list.
+// for the one-query sequences, then the prefill work list and its queues.
 size_t prefill_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads, int max_context) {
   return balanced_workspace(waves, groups, head_dim, batch, num_kv_heads) +
-         align256(prefill_work_entries(batch, max_context) * sizeof(int));
+         align256(prefill_work_entries(batch, max_context) * sizeof(int)) + align256((kPrefillQueues + 1) * sizeof(int));
 }
 
 extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,
@@ -295,6 +295,9 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
       return fail(LI_EWORKSPACE, "li_paged_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
     a.work = reinterpret_cast<int*>(static_cast<char*>(workspace) +
                                     balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads));
+    a.queue = reinterpret_cast<int*>(reinterpret_cast<char*>(a.work) +
+                                     align256(prefill_work_entries(batch, max_context) * sizeof(int)));
+    if (flags & LI_FLAG_PREFILL_ONLY) return launch_prefill_mfma(a, dtype, s);
     AttnArgs d = a;
     d.block_q = 1;
     d.num_qblocks = 1;

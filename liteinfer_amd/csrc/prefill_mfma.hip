@@ -100,18 +100,35 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, uniform
   const int n = lane & 15, g = lane >> 4;
 
-  const int item = a.work[blockIdx.x / a.num_kv_heads];
-  if (item < 0) return;  // past the list's end
+  // Persistent grid: work-groups take (query block, KV head) units from
+  // their queue until it runs dry. With num_kv_heads a multiple of 8 there
+  // is one queue per XCD (work-group i runs on XCD i % 8) holding the units
+  // of KV heads q, q + 8, ..., so every block of one KV head is folded on one
+  // XCD and reuses that head's K/V from its L2; otherwise one queue. Units
+  // come in the work list's order, heaviest block first: a work-group that
+  // finishes early takes the next heaviest unit left.
+  const int nqueues = a.num_kv_heads % kPrefillQueues == 0 ? kPrefillQueues : 1;
+  const int qi = blockIdx.x % nqueues;
+  const int heads_per_queue = a.num_kv_heads / nqueues;
+  const int units = a.queue[kPrefillQueues] * heads_per_queue;
+  __shared__ int s_unit;
+  for (;;) {
+  __syncthreads();  // every wave is done with the previous unit's LDS
+  if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
+  __syncthreads();
+  const int unit = s_unit;
+  if (unit >= units) break;
+  const int item = a.work[unit / heads_per_queue];
   const int seq = item / a.num_qblocks;
   const int qblock = item % a.num_qblocks;
-  const int kvh = blockIdx.x % a.num_kv_heads;
+  const int kvh = qi + nqueues * (unit % heads_per_queue);
 
   const int first_tok = a.qsl[seq];
   const int nq = a.qsl[seq + 1] - first_tok;
   const int bq = a.block_q;  // query tokens per block = 32 W / groups
   const int q0 = qblock * bq;
-  if (q0 >= nq) return;
-  if (nq == 1 && a.single_query_elsewhere) return;  // the decode kernel serves it
+  if (q0 >= nq) continue;
+  if (nq == 1 && a.single_query_elsewhere) continue;  // the decode kernel serves it
   const int q1 = min(q0 + bq, nq);
   const int ctx = a.ctx[seq];
   const int pos0 = ctx - nq;   // position of the sequence's first query
@@ -329,6 +346,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
       *reinterpret_cast<uint2*>(orow + 16 * blk) = wv;
     }
   }
+  }  // units
 }
 
 // Work list of the prefill grid: every non-empty query block
@@ -393,6 +411,9 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
     if (t > 0) a.work[atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], 1)] = it;
   }
   for (int i = max_tiles + tid; i < items; i += 1024) a.work[i] = -1;
+  // The persistent grid's queues start empty for this launch.
+  if (tid < kPrefillQueues) a.queue[tid] = 0;
+  if (tid == 0) a.queue[kPrefillQueues] = max_tiles;
 }
 
 bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
@@ -419,20 +440,24 @@ template <int W>
 static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
   a.block_q = 32 * W / a.groups;
   a.num_qblocks = cdiv(a.max_query_len, a.block_q);
-  const int64_t blocks = (int64_t)a.batch * a.num_kv_heads * a.num_qblocks;
-  if (blocks == 0) return LI_OK;
-  if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "prefill grid of %lld blocks is too large", (long long)blocks);
+  const int64_t units = (int64_t)a.batch * a.num_kv_heads * a.num_qblocks;
+  if (units == 0) return LI_OK;
   if ((size_t)a.batch * a.num_qblocks > prefill_work_entries(a.batch, a.max_context))
     return fail(LI_EINVAL, "prefill: %d query blocks per sequence exceed the planned work list", a.num_qblocks);
   hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
   if (int rc = check_launch("prefill_order")) return rc;
-  const dim3 grid((unsigned)blocks), block(64 * W);
+  // One work-group per CU (its LDS and registers fill one), a multiple of
+  // the queue count so every queue has work-groups, and never more than
+  // there can be units.
+  int64_t grid = (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues;
+  grid = std::min<int64_t>(grid, (units + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues);
+  const dim3 block(64 * W);
   if (dtype == LI_BF16) {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64, W>), grid, block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W>), dim3((unsigned)grid), block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64, W>), dim3((unsigned)grid), block, 0, s, a);
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64, W>), grid, block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W>), dim3((unsigned)grid), block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64, W>), dim3((unsigned)grid), block, 0, s, a);
   }
   return check_launch("prefill_mfma");
 }

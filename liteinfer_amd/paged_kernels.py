@@ -270,6 +270,7 @@ def paged_prefill(
     block_q: int = _PREFILL_BLOCK_Q,
     *,
     kernel: str = "auto",
+    one_query_rows: bool | None = None,
 ) -> torch.Tensor:
     """Attend each sequence's chunk of queries over the KV its slots address, causally.
 
@@ -291,6 +292,10 @@ def paged_prefill(
         num_kv_groups: query heads per KV head.
         block_kv, block_q: tiles of the general-shape kernel.
         kernel: ``"auto"`` (MFMA where it applies) or ``"generic"``.
+        one_query_rows: whether any sequence brings a single query (``None``:
+            unknown). The MFMA path hands those to the split decode kernel;
+            ``False`` lets the prefill kernel serve every sequence and skips
+            the decode launch. Either way the result is the same attention.
 
     Returns:
         ``[total_queries, num_heads, head_dim]`` with the strides of `query`.
@@ -337,7 +342,9 @@ def paged_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
         num_heads, num_kv_heads, head_dim, float(scaling), block_q, block_kv,
         workspace.data_ptr() if workspace is not None else None, need.value,
-        _native.dtype_code(query.dtype), _flags(_prefill_kernel(kernel)), _native.stream_handle(device),
+        _native.dtype_code(query.dtype),
+        _flags(_prefill_kernel(kernel)) | (_native.LI_FLAG_PREFILL_ONLY if one_query_rows is False else 0),
+        _native.stream_handle(device),
     )
     _native.check(status, "paged_prefill")
     return out

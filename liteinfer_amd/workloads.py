@@ -150,6 +150,17 @@ def decode_step(config: str, dtype=torch.bfloat16, device="cuda", seed: int = 0,
     )
 
 
+def c3_shapes(seed: int = 0) -> tuple[list[tuple[int, int]], list[int]]:
+    """Config 3's (queries, cached prefix) chunks and its decode-row contexts, as packed_step draws them."""
+    return _c3_shapes(np.random.default_rng(seed))
+
+
+def _c3_shapes(rng: np.random.Generator) -> tuple[list[tuple[int, int]], list[int]]:
+    chunks = list(zip(rng.integers(64, 2048 + 1, size=8).tolist(), rng.integers(0, 4096 + 1, size=8).tolist()))
+    decode_contexts = rng.integers(256, 4096 + 1, size=56).tolist()
+    return [(int(q), int(p)) for q, p in chunks], [int(c) for c in decode_contexts]
+
+
 def packed_step(config: str = "c3", dtype=torch.bfloat16, device="cuda", seed: int = 0,
                 chunks: list[tuple[int, int]] | None = None, decode_contexts: list[int] | None = None,
                 geometry: Geometry = LLAMA_3_8B, num_blocks: int = 65536) -> PackedStep:
@@ -159,8 +170,7 @@ def packed_step(config: str = "c3", dtype=torch.bfloat16, device="cuda", seed: i
     gen = torch.Generator(device=device).manual_seed(seed)
     geo = geometry
     if config == "c3":
-        chunks = list(zip(rng.integers(64, 2048 + 1, size=8).tolist(), rng.integers(0, 4096 + 1, size=8).tolist()))
-        decode_contexts = rng.integers(256, 4096 + 1, size=56).tolist()
+        chunks, decode_contexts = _c3_shapes(rng)
     elif config != "custom":
         raise ValueError(f"unknown packed config {config!r}")
     chunks = [(int(q), int(p)) for q, p in (chunks or [])]

@@ -89,9 +89,30 @@ def test_bfloat16_within_rounding(kernel):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim", [64, 128])
-@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (8, 8), (10, 2), (16, 1)])
-def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads):
-    """Chunks straddling every tile boundary, over prefixes and alone, beside decode rows."""
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (8, 8), (10, 2), (16, 1), (32, 16)])
+@pytest.mark.parametrize("one_query_rows", [None, False])
+def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads, one_query_rows):
+    """Chunks straddling every tile boundary, over prefixes and alone, beside decode rows.
+
+    ``one_query_rows=False`` has the prefill kernel serve the one-query
+    sequences too (the decode kernel is not launched): same answer.
+    """
     b = PagedBatch([1, 40, 300, 129, 64, 700], [1, 33, 200, 1, 64, 31], dtype=dtype, num_heads=num_heads,
                    num_kv_heads=num_kv_heads, head_dim=head_dim, num_slots=4096, seed=6)
-    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+    assert_within(_run(b, one_query_rows=one_query_rows), b.oracle(), 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (32, 16), (8, 2)])
+def test_persistent_grid_takes_every_unit_on_every_call(num_heads, num_kv_heads):
+    """More (query block, KV head) units than work-groups, in per-XCD queues or one
+    queue; the queues restart empty on every launch, so repeated calls agree bit for bit."""
+    rng = np.random.default_rng(11)
+    q = rng.integers(1, 200, size=24).tolist()
+    p = rng.integers(0, 300, size=24).tolist()
+    b = PagedBatch([qq + pp for qq, pp in zip(q, p)], q, dtype=torch.bfloat16, num_heads=num_heads,
+                   num_kv_heads=num_kv_heads, head_dim=128, num_slots=32768, seed=12)
+    first = _run(b)
+    assert_within(first, b.oracle(), 2 ** -6, 2e-3)
+    for _ in range(3):
+        again = _run(b)
+        assert torch.equal(again, first)
