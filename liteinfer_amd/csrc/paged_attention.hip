@@ -285,10 +285,11 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!(flags & LI_FLAG_FORCE_GENERIC) && prefill_mfma_applies(a, dtype)) {
-    // One-query sequences (decode rows beside chunks) would leave 127 of a
-    // prefill block's 128 rows idle and walk their whole context in one
+    // One-query sequences (decode rows beside chunks) would leave all but G
+    // of a prefill unit's 256 rows idle and walk their whole context in one
     // work-group; the decode kernel serves them instead, its key axis cut
-    // into partitions, and the prefill kernel skips them.
+    // into partitions, and the prefill kernel skips them (unless the caller
+    // says there are none: LI_FLAG_PREFILL_ONLY).
     const int waves = balanced_waves(device_cu_count());
     const size_t need = prefill_workspace(waves, a.groups, head_dim, batch, num_kv_heads, max_context);
     if (!workspace || workspace_bytes < need)

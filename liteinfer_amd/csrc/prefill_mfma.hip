@@ -7,36 +7,43 @@
 // keys up to its own position, the online softmax runs in fp32 and the
 // weights are rounded to the value dtype before they multiply V.
 //
-// One workgroup of 4 waves per (sequence, KV head, block of 128 / G query
-// tokens). Its 128 rows are (query token, head) pairs, head fastest, so the G
-// heads that share a KV head read each K/V tile once; wave w owns rows
-// 32w..32w+31 as two 16-row MFMA blocks. The keys [0, last query's
-// position] stream through LDS 64 at a time, loaded straight into LDS by all
-// four waves (two stages, so the next 64 keys land while these are folded),
-// in the 32-key tile layout the decode kernel uses (li_mfma.h). Per 32 keys
-// and 16 rows:
+// A unit of work is (sequence, KV head, block of 256 / G query tokens),
+// folded by one work-group of 8 waves (two per SIMD). Its 256 rows are
+// (query token, head) pairs, head fastest, so the G heads that share a KV
+// head read each K/V tile once; wave w owns rows 32w..32w+31 as two 16-row
+// MFMA blocks. The keys [0, last query's position] stream through LDS 64 at
+// a time, loaded straight into LDS by all eight waves (two stages, so the
+// next 64 keys land while these are folded), in the 32-key tile layout of
+// li_mfma.h. Per stage and 16 rows:
 //
 //   S^T = K Q^T     A = K rows from LDS, B = the rows' Q^T kept in registers.
-//                   Lane (n, g) gets the scores of keys {4g..4g+3,
-//                   16+4g..16+4g+3} for row n.
-//   O^T += V^T P^T  B = P^T is those 8 weights as they are; A = V^T comes
-//                   straight out of LDS through transposing reads
-//                   (ds_read_b64_tr_b16, li_read_vt), shared by both row
-//                   blocks. One more MFMA against a block of ones gives each
-//                   row's sum of weights.
+//                   Lane (n, g) gets the scores of keys 16b + 4g .. + 3 of
+//                   key block b = 0..3 for row n.
+//   softmax         one running-max update per row over all 64 keys.
+//   O^T += V^T P^T  B = P^T is a 32-key tile's 8 weights as they are; A =
+//                   V^T comes straight out of LDS through transposing reads
+//                   (ds_read_b64_tr_b16, li_read_vt's addressing), shared by
+//                   both row blocks. One more MFMA against a block of ones
+//                   gives each row's sum of weights.
+//
+// Every LDS read is one instruction from a per-lane address fixed for the
+// whole kernel plus an immediate offset (the loop body covers both stages,
+// so stage bases are constants).
 //
 // A row's visibility is key <= its position; the mask is a compare per
-// score, applied only to tiles that reach past the block's first query
+// score, applied only to stages that reach past the block's first query
 // position (the diagonal). Padding rows (past the block or the sequence) see
-// every key with a zero query, so they stay finite, and are never stored.
+// every key with a zero query, so they stay finite, and are never stored; a
+// wave whose rows are all padding only helps load the stages.
 //
-// Grid order: work-group i takes query block work[i / num_kv_heads] (a list
-// prefill_order sorts longest first) and KV head i % num_kv_heads. Work-groups
-// are dispatched in grid order as earlier ones retire, so the longest blocks
-// start first and short ones fill in behind them; and with num_kv_heads a
-// multiple of 8 every block of one KV head lands on the same XCD
-// (work-groups are dealt to the 8 XCDs round robin) and reuses that head's
-// K/V from the XCD's L2.
+// Scheduling: a persistent grid of one work-group per CU. prefill_order
+// lists every non-empty query block, heaviest first; work-groups pull
+// (block, KV head) units from queues in that order through an atomic
+// counter, so long units start first, short ones fill in behind, and no
+// work-group is launched for an empty block. With num_kv_heads a multiple of
+// 8 there is one queue per XCD (work-group i runs on XCD i % 8) holding the
+// KV heads q, q + 8, ...: every block of one KV head is folded on one XCD and
+// reuses that head's K/V from the XCD's L2.
 #include "li_attention.h"
 #include "li_mfma.h"
 
