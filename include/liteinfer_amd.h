@@ -35,8 +35,10 @@
 extern "C" {
 #endif
 
-/* Element types of q / pools / out. */
-enum li_dtype { LI_F32 = 0, LI_F16 = 1, LI_BF16 = 2 };
+/* Element types of q / pools / out. LI_FP8_E4M3 (OCP e4m3, one byte) is a
+   pool type only: its rows hold K / k_scale and V / v_scale (see
+   li_kv_scatter_fp8 and the _ex entry points). */
+enum li_dtype { LI_F32 = 0, LI_F16 = 1, LI_BF16 = 2, LI_FP8_E4M3 = 3 };
 
 /* Error codes. */
 enum li_status {
@@ -87,6 +89,23 @@ int li_kv_scatter(const void* k, const void* v, const int64_t* k_strides,
                   int64_t num_slots, int64_t pool_stride_slot,
                   int64_t pool_stride_head, int num_kv_heads, int head_dim,
                   int dtype, void* stream);
+
+/*
+ * Quantising KV slot-write into an fp8 (LI_FP8_E4M3) pool: the reference's
+ * planned quantised cache (liteinfer docs/roadmap.md, section 2.5:
+ * "storage-level quant of K and V; dequant on read"), write side. Same
+ * layout contract as li_kv_scatter, with each element stored as
+ *     e4m3(clamp(float(x) * (1 / scale), -448, 448))
+ * (the reciprocal in fp32, round to nearest even), k and v of src_dtype
+ * (LI_F32 / LI_F16 / LI_BF16). The readers multiply back by the scale. No
+ * counterpart in the reference's code: its cache is never quantised.
+ */
+int li_kv_scatter_fp8(const void* k, const void* v, const int64_t* k_strides,
+                      const int64_t* v_strides, int64_t batch, int64_t tokens,
+                      const int64_t* slots, void* key_pool, void* value_pool,
+                      int64_t num_slots, int64_t pool_stride_slot,
+                      int64_t pool_stride_head, int num_kv_heads, int head_dim,
+                      int src_dtype, float k_scale, float v_scale, void* stream);
 
 /*
  * Fused rotary embedding + KV slot-write. Replaces, per layer, the
@@ -160,6 +179,27 @@ int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
                     int num_heads, int num_kv_heads, int head_dim, float scale,
                     int num_splits, int block_kv, void* workspace,
                     size_t workspace_bytes, int dtype, int flags, void* stream);
+
+/*
+ * li_paged_decode over a pool of element type kv_dtype: `dtype` (then the
+ * scales are ignored and this is li_paged_decode) or LI_FP8_E4M3, whose rows
+ * hold K / k_scale and V / v_scale as written by li_kv_scatter_fp8. The
+ * result is the attention over the dequantised rows; pool strides are in
+ * pool elements (bytes for fp8). fp8 pools run on the MFMA kernel only
+ * (bf16 / fp16 queries, head_dim 128; otherwise LI_EUNSUPPORTED). Carries the
+ * reference's planned dequant-on-read (docs/roadmap.md, section 2.5); no
+ * counterpart in the reference's code.
+ */
+int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+                       const void* key_pool, const void* value_pool,
+                       int64_t pool_stride_slot, int64_t pool_stride_head,
+                       const int64_t* slot_table, int64_t slot_table_stride,
+                       int max_context, const int32_t* context_lens, void* out,
+                       int64_t out_stride_seq, int64_t out_stride_head, int batch,
+                       int num_heads, int num_kv_heads, int head_dim, float scale,
+                       int num_splits, int block_kv, void* workspace,
+                       size_t workspace_bytes, int dtype, int kv_dtype,
+                       float k_scale, float v_scale, int flags, void* stream);
 
 /*
  * Workspace bytes li_paged_prefill needs for a pass of `batch` sequences over

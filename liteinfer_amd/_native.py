@@ -16,7 +16,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libliteinfer_amd.so"
 
-LI_F32, LI_F16, LI_BF16 = 0, 1, 2
+LI_F32, LI_F16, LI_BF16, LI_FP8_E4M3 = 0, 1, 2, 3
 LI_OK, LI_EINVAL, LI_EUNSUPPORTED, LI_ELAUNCH, LI_EWORKSPACE = 0, -1, -2, -3, -4
 LI_FLAG_FORCE_GENERIC = 1
 LI_FLAG_EQUAL_SPLITS = 2
@@ -24,15 +24,21 @@ LI_FLAG_PREFILL_ONLY = 4
 
 DTYPE_CODES = {torch.float32: LI_F32, torch.float16: LI_F16, torch.bfloat16: LI_BF16}
 
+# The pool element type of a quantised cache (OCP e4m3: what gfx950's fp8
+# conversions implement).
+FP8_POOL_DTYPE = torch.float8_e4m3fn
+
 # Every symbol the header declares, in declaration order.
 EXPORTED_SYMBOLS = (
     "li_last_error_string",
     "li_abi_version",
     "li_kv_scatter",
+    "li_kv_scatter_fp8",
     "li_rope_kv_write",
     "li_choose_num_splits",
     "li_paged_decode_plan",
     "li_paged_decode",
+    "li_paged_decode_ex",
     "li_paged_prefill_plan",
     "li_paged_prefill",
 )
@@ -46,6 +52,10 @@ _SIGNATURES = {
     "li_kv_scatter": (
         _i32,
         [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p],
+    ),
+    "li_kv_scatter_fp8": (
+        _i32,
+        [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _f32, _f32, _p],
     ),
     "li_rope_kv_write": (
         _i32,
@@ -63,6 +73,11 @@ _SIGNATURES = {
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _p],
     ),
+    "li_paged_decode_ex": (
+        _i32,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
+         _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _f32, _f32, _i32, _p],
+    ),
     "li_paged_prefill_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)]),
     "li_paged_prefill": (
         _i32,
@@ -71,7 +86,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

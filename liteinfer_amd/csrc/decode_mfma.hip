@@ -34,18 +34,27 @@
 #include "li_attention.h"
 #include "li_mfma.h"
 
+#include <type_traits>
+
 #include <cstdlib>
 
 namespace li {
 namespace {
 
+// The LDS tile layout of a pool: bf16 / fp16 rows, or fp8 (e4m3) rows at
+// head_dim 128.
+template <int D, bool F8>
+using KvTile = std::conditional_t<F8, F8Tile, TileLayout<D>>;
+
 // Issues the 2 * kInsts direct-to-LDS loads of the 32-key tile whose first
 // key is entry `t` of the staged slots, into the stage at `stage`. Lane
-// (rr, n) = (lane / CH, lane % CH) loads keys rr * kInsts + i.
-template <typename T, int D>
-__device__ __forceinline__ void issue_tile(char* stage, const T* __restrict__ kpool, const T* __restrict__ vpool,
-                                           const int* __restrict__ sl, int64_t p_s0, int t, int lane) {
-  using L = TileLayout<D>;
+// (rr, n) = (lane / CH, lane % CH) loads keys rr * kInsts + i. kpool / vpool
+// point at the KV head's row of slot 0, row_bytes is the pool's slot stride.
+template <int D, bool F8>
+__device__ __forceinline__ void issue_tile(char* stage, const char* __restrict__ kpool,
+                                           const char* __restrict__ vpool, const int* __restrict__ sl,
+                                           uint32_t row_bytes, int t, int lane) {
+  using L = KvTile<D, F8>;
   const int rr = lane / L::kCh, nn = lane % L::kCh;
   int keys[L::kInsts];
   if constexpr (L::kInsts == 8) {
@@ -61,18 +70,17 @@ __device__ __forceinline__ void issue_tile(char* stage, const T* __restrict__ kp
   for (int i = 0; i < L::kInsts; ++i) {
     const int key = rr * L::kInsts + i;
     const uint32_t dst = lds_addr(stage + i * 1024);  // rows kRowsPerInst * i ..: 1 KiB per instruction
-    const uint32_t row_bytes = (uint32_t)(p_s0 * sizeof(T));
     // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
-    dma16(row_ptr(kpool + 8 * (nn ^ (key % L::kCh)), (uint32_t)keys[i], row_bytes), dst);
-    dma16(row_ptr(vpool + 8 * (nn ^ L::vswizzle(key)), (uint32_t)keys[i], row_bytes), dst + 32 * L::kRowBytes);
+    dma16(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), (uint32_t)keys[i], row_bytes), dst);
+    dma16(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), (uint32_t)keys[i], row_bytes), dst + 32 * L::kRowBytes);
   }
 }
 
 // LDS of one decode wave: the staged slots of a chunk and two tile stages.
-template <int D>
+template <int D, bool F8>
 struct DecodeLds {
   int sl[kSlotChunk + 64];
-  char stage[2][TileLayout<D>::kTileBytes];
+  char stage[2][KvTile<D, F8>::kTileBytes];
 };
 
 // Online-softmax state of one wave: lane (n, g) holds head n's running max
@@ -85,29 +93,40 @@ struct DecodeState {
 
 // Folds keys [kb, ke) of sequence `seq`'s context for KV head `kvh` into `st`.
 // qf holds this lane's head's query (zeros for heads past the group).
-template <typename T, int D>
-__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, const typename Mfma<T>::Frag* qf,
+template <typename T, int D, bool F8>
+__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& lds, const typename Mfma<T>::Frag* qf,
                                           int seq, int kvh, int kb, int ke, DecodeState& st) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
-  using L = TileLayout<D>;
+  using L = KvTile<D, F8>;
   constexpr int kSteps = D / 32;
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
   // Per-lane LDS byte offsets within a tile: the K operand of key n, step j
-  // (key 16 + n sits L::kRow16 bytes below), and li_read_vt's V^T addresses.
+  // (key 16 + n sits L::kRow16 bytes below), and the V^T reads' addresses
+  // (li_read_vt's two for 16-bit rows, the one 8-bit transposing read for
+  // fp8 rows; see F8Tile).
   uint32_t koff[kSteps], voff[D / 16];
+  if constexpr (F8) {
 #pragma unroll
-  for (int j = 0; j < kSteps; ++j) koff[j] = L::offset(n, 4 * j + g);
-  {
+    for (int j = 0; j < kSteps; ++j) koff[j] = L::offset(n, 2 * j + (g >> 1)) + 8 * (g & 1);
+    const int s16 = lane & 15;
+#pragma unroll
+    for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(kappa(g, s16 >> 1), blk) + 8 * (s16 & 1);
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) koff[j] = L::offset(n, 4 * j + g);
     const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
 #pragma unroll
     for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
   }
-  const T* kpool = static_cast<const T*>(a.kp) + (int64_t)kvh * a.p_s1;
-  const T* vpool = static_cast<const T*>(a.vp) + (int64_t)kvh * a.p_s1;
+  const int esize = F8 ? 1 : (int)sizeof(T);  // bytes per pool element
+  const char* kpool = static_cast<const char*>(a.kp) + (int64_t)kvh * a.p_s1 * esize;
+  const char* vpool = static_cast<const char*>(a.vp) + (int64_t)kvh * a.p_s1 * esize;
+  const uint32_t row_bytes = (uint32_t)(a.p_s0 * esize);
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
-  const float sc = a.scale * kLog2eMfma;
+  // An fp8 pool stores K / k_scale: its scale multiplies the scores.
+  const float sc = a.scale * (F8 ? a.k_scale : 1.f) * kLog2eMfma;
 
   for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
     const int c1 = min(c0 + kSlotChunk, ke);
@@ -129,8 +148,13 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
       floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < kSteps; ++j) {
-        s0 = M::mma(lds_read_frag<Frag>(stage + koff[j]), qf[j], s0);
-        s1 = M::mma(lds_read_frag<Frag>(stage + koff[j] + L::kRow16), qf[j], s1);
+        if constexpr (F8) {
+          s0 = M::mma(lds_read_f8_frag<Frag>(stage + koff[j]), qf[j], s0);
+          s1 = M::mma(lds_read_f8_frag<Frag>(stage + koff[j] + L::kRow16), qf[j], s1);
+        } else {
+          s0 = M::mma(lds_read_frag<Frag>(stage + koff[j]), qf[j], s0);
+          s1 = M::mma(lds_read_frag<Frag>(stage + koff[j] + L::kRow16), qf[j], s1);
+        }
       }
       float x[8];
 #pragma unroll
@@ -168,8 +192,10 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
       // O^T += V^T P^T, 16 dims at a time, V^T straight out of LDS.
       const uint32_t vstage = stage + 32 * L::kRowBytes;
 #pragma unroll
-      for (int blk = 0; blk < D / 16; ++blk)
-        st.acc[blk] = M::mma(lds_read_vt<Frag>(vstage + voff[blk], vstage + voff[blk] + L::kRow16), pf, st.acc[blk]);
+      for (int blk = 0; blk < D / 16; ++blk) {
+        if constexpr (F8) st.acc[blk] = M::mma(lds_read_f8_vt<Frag>(vstage + voff[blk]), pf, st.acc[blk]);
+        else st.acc[blk] = M::mma(lds_read_vt<Frag>(vstage + voff[blk], vstage + voff[blk] + L::kRow16), pf, st.acc[blk]);
+      }
     };
 
     // Two stages: while one tile is folded the next tile's loads land in the
@@ -177,13 +203,13 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D>& lds, 
     // so the loads in flight are the same every step and no load sits under
     // a branch.
     constexpr int kInFlight = 2 * L::kInsts;
-    issue_tile<T, D>(lds.stage[0], kpool, vpool, lds.sl, a.p_s0, 0, lane);
+    issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, 0, lane);
     for (int ti = 0;;) {
-      issue_tile<T, D>(lds.stage[1], kpool, vpool, lds.sl, a.p_s0, min(32 * (ti + 1), kSlotChunk), lane);
+      issue_tile<D, F8>(lds.stage[1], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
       fold(lds_addr(lds.stage[0]), c0 + 32 * ti);
       if (++ti >= ntiles) break;
-      issue_tile<T, D>(lds.stage[0], kpool, vpool, lds.sl, a.p_s0, min(32 * (ti + 1), kSlotChunk), lane);
+      issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
       fold(lds_addr(lds.stage[1]), c0 + 32 * ti);
       if (++ti >= ntiles) break;
@@ -207,15 +233,16 @@ __device__ __forceinline__ void load_query(const AttnArgs& a, int row, int kvh, 
 // Writes a finished softmax: the normalised output row of each head of the
 // group to `out` (dtype T), or, for a piece of a context, the fp32 normalised
 // partial of head n to po + n * p_head_stride * D and its log2-domain LSE to
-// plse[n * p_head_stride].
+// plse[n * p_head_stride]. vscale multiplies the outputs (an fp8 pool stores
+// V / v_scale).
 template <typename T, int D>
 __device__ __forceinline__ void store_state(const DecodeState& st, T* orow_head0, int64_t o_s1, float* po,
-                                            float* plse, int64_t p_head_stride, int groups) {
+                                            float* plse, int64_t p_head_stride, int groups, float vscale) {
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
   const float lt = li_group_sum(st.l);
   if (n >= groups) return;
-  const float inv = 1.f / lt;
+  const float inv = vscale / lt;
   if (orow_head0) {
     T* orow = orow_head0 + (int64_t)n * o_s1 + 4 * g;
 #pragma unroll
@@ -263,10 +290,11 @@ __device__ __forceinline__ int decode_keys(const AttnArgs& a, int seq) {
 // pinned split count (the reference's equal-slice rule: partition p of a
 // context of c keys is [p * cdiv(c, S), ...)).
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+template <typename T, int D, bool F8>
 __global__ __launch_bounds__(64) void decode_partitioned(AttnArgs a) {
   using Frag = typename Mfma<T>::Frag;
-  __shared__ __attribute__((aligned(1024))) DecodeLds<D> lds;
+  __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds;
+  const float vscale = F8 ? a.v_scale : 1.f;
   // Partition-major order: every sequence's first partition is dispatched
   // before any second one, so the grid's empty tail comes last.
   int bid = blockIdx.x;
@@ -287,15 +315,15 @@ __global__ __launch_bounds__(64) void decode_partitioned(AttnArgs a) {
   load_query<T, D>(a, row, kvh, qf);
   DecodeState st;
   reset_state(st);
-  fold_keys<T, D>(a, lds, qf, seq, kvh, kb, ke, st);
+  fold_keys<T, D, F8>(a, lds, qf, seq, kvh, kb, ke, st);
   const int head0 = kvh * a.groups;
   if (nparts == 1) {
     store_state<T, D>(st, static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head0 * a.o_s1, a.o_s1,
-                      nullptr, nullptr, 0, a.groups);
+                      nullptr, nullptr, 0, a.groups, vscale);
   } else {
     // partials [batch, num_heads, num_parts, D]: head h's row is (seq * Hq + h) * P + part
     const int64_t base = ((int64_t)seq * a.num_heads + head0) * a.num_parts + part;
-    store_state<T, D>(st, nullptr, 0, a.part_o + base * D, a.part_lse + base, a.num_parts, a.groups);
+    store_state<T, D>(st, nullptr, 0, a.part_o + base * D, a.part_lse + base, a.num_parts, a.groups, vscale);
   }
 }
 
@@ -336,10 +364,11 @@ __device__ __forceinline__ void balanced_share(const AttnArgs& a, int64_t& total
   share = ((total + waves - 1) / waves + 31) / 32 * 32;
 }
 
-template <typename T, int D>
+template <typename T, int D, bool F8>
 __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
   using Frag = typename Mfma<T>::Frag;
-  __shared__ __attribute__((aligned(1024))) DecodeLds<D> lds;
+  __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds;
+  const float vscale = F8 ? a.v_scale : 1.f;
   const int lane = threadIdx.x;
   const int w = blockIdx.x;
   int64_t total, share;
@@ -394,13 +423,13 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
     load_query<T, D>(a, row, kvh, qf);
     DecodeState st;
     reset_state(st);
-    fold_keys<T, D>(a, lds, qf, seq, kvh, key0, key0 + take, st);
+    fold_keys<T, D, F8>(a, lds, qf, seq, kvh, key0, key0 + take, st);
     if (key0 == 0 && take == ctx) {
       store_state<T, D>(st, static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)kvh * G * a.o_s1, a.o_s1,
-                        nullptr, nullptr, 0, G);
+                        nullptr, nullptr, 0, G, vscale);
     } else {
       const int slot = first_segment ? 0 : 1;
-      store_state<T, D>(st, nullptr, 0, part_o + (int64_t)slot * G * a.head_dim, part_lse + slot * G, 1, G);
+      store_state<T, D>(st, nullptr, 0, part_o + (int64_t)slot * G * a.head_dim, part_lse + slot * G, 1, G, vscale);
     }
     pos += take;
     first_segment = false;
@@ -488,9 +517,11 @@ bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
 bool decode_mfma_applies(const AttnArgs& a, int dtype) {
   if (dtype != LI_BF16 && dtype != LI_F16) return false;
   if (a.head_dim != 64 && a.head_dim != 128) return false;
+  if (a.kv_fp8 && a.head_dim != 128) return false;
   if (a.groups < 1 || a.groups > 16) return false;
+  const int pe = a.kv_fp8 ? 1 : 2;
   return rows_aligned(a.q, a.q_s0, a.q_s1, 2) && rows_aligned(a.out, a.o_s0, a.o_s1, 2) &&
-         rows_aligned(a.kp, a.p_s0, a.p_s1, 2) && rows_aligned(a.vp, a.p_s0, a.p_s1, 2);
+         rows_aligned(a.kp, a.p_s0, a.p_s1, pe) && rows_aligned(a.vp, a.p_s0, a.p_s1, pe);
 }
 
 int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
@@ -499,17 +530,20 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
   if (blocks == 0) return LI_OK;
   if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "decode grid of %lld blocks is too large", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(64);
-#define LI_DECODE_LAUNCH(T, D)                                                   \
-  do {                                                                           \
-    if (balanced) hipLaunchKernelGGL((decode_balanced<T, D>), grid, block, 0, s, a); \
-    else hipLaunchKernelGGL((decode_partitioned<T, D>), grid, block, 0, s, a);       \
+#define LI_DECODE_LAUNCH(T, D, F8)                                                        \
+  do {                                                                                    \
+    if (balanced) hipLaunchKernelGGL((decode_balanced<T, D, F8>), grid, block, 0, s, a);  \
+    else hipLaunchKernelGGL((decode_partitioned<T, D, F8>), grid, block, 0, s, a);        \
   } while (0)
-  if (dtype == LI_BF16) {
-    if (a.head_dim == 128) LI_DECODE_LAUNCH(li_bf16, 128);
-    else LI_DECODE_LAUNCH(li_bf16, 64);
+  if (a.kv_fp8) {
+    if (dtype == LI_BF16) LI_DECODE_LAUNCH(li_bf16, 128, true);
+    else LI_DECODE_LAUNCH(li_f16, 128, true);
+  } else if (dtype == LI_BF16) {
+    if (a.head_dim == 128) LI_DECODE_LAUNCH(li_bf16, 128, false);
+    else LI_DECODE_LAUNCH(li_bf16, 64, false);
   } else {
-    if (a.head_dim == 128) LI_DECODE_LAUNCH(li_f16, 128);
-    else LI_DECODE_LAUNCH(li_f16, 64);
+    if (a.head_dim == 128) LI_DECODE_LAUNCH(li_f16, 128, false);
+    else LI_DECODE_LAUNCH(li_f16, 64, false);
   }
 #undef LI_DECODE_LAUNCH
   if (int rc = check_launch("decode_mfma")) return rc;

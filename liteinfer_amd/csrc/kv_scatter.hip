@@ -98,6 +98,8 @@ extern "C" int li_kv_scatter(const void* k, const void* v, const int64_t* k_stri
   li::clear_error();
   const int esize = li::dtype_size(dtype);
   if (esize == 0) return li::fail(LI_EINVAL, "li_kv_scatter: unknown dtype %d", dtype);
+  if (dtype == LI_FP8_E4M3)
+    return li::fail(LI_EUNSUPPORTED, "li_kv_scatter: fp8 pools are written by li_kv_scatter_fp8 (quantising), not copied");
   if (batch < 0 || tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || num_slots < 0)
     return li::fail(LI_EINVAL, "li_kv_scatter: negative or empty extent (batch=%lld tokens=%lld heads=%d dim=%d)",
                     (long long)batch, (long long)tokens, num_kv_heads, head_dim);

@@ -43,6 +43,11 @@ struct AttnArgs {
   int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
   int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
   int* queue;    // MFMA prefill: kPrefillQueues unit counters, then the number of blocks listed in `work`
+  // fp8 (e4m3) pools: kp / vp hold K / k_scale and V / v_scale, one byte per
+  // element (pool strides in bytes); the MFMA kernels only. Other pools hold
+  // the query's dtype and ignore the scales.
+  int kv_fp8;
+  float k_scale, v_scale;
 };
 
 // Work queues of the persistent MFMA prefill grid (one per XCD).

@@ -31,6 +31,7 @@ inline int dtype_size(int dtype) {
     case LI_F32: return 4;
     case LI_F16: return 2;
     case LI_BF16: return 2;
+    case LI_FP8_E4M3: return 1;
     default: return 0;
   }
 }

@@ -49,6 +49,7 @@ struct TileLayout {
   // Key k + 16 sits this many bytes below key k (same swizzle: kCh divides 16).
   static constexpr int kRow16 = (16 / kInsts) * kRowBytes;
   __device__ static int row_of(int key) { return kRowsPerInst * (key % kInsts) + key / kInsts; }
+  __device__ static int kswizzle(int key) { return key % kCh; }
   __device__ static int offset(int key, int chunk) {  // byte offset within the K half
     return row_of(key) * kRowBytes + 16 * (chunk ^ (key % kCh));
   }
@@ -64,6 +65,69 @@ struct TileLayout {
     return row_of(key) * kRowBytes + 16 * (chunk ^ vswizzle(key));
   }
 };
+
+// The 32-key tile of an fp8 (e4m3) pool at head_dim 128: rows of 128 bytes
+// (8 chunks of 16), K then V, filled by the same direct-to-LDS loads
+// (instruction i, row-in-instruction rr holds key rr * 4 + i). Operands are
+// read 8 bytes at a time: the K operand of key n at step j is chunk
+// 2j + g / 2, half g % 2 (ds_read_b64); the V^T operand of 16 dims comes
+// from one 8-bit transposing read (ds_read_b64_tr_b8), which gives lane
+// 8h + t of a 16-lane group byte t of the reads of lanes h, h + 2, ...,
+// h + 14, so lane s reads half s % 2 of the dims' chunk of key
+// kappa(g, s / 2) and lane m receives dim 16 blk + m of keys kappa(g, 0..7).
+// Rows alternate bank halves (128 bytes per row, 256 bytes per bank row), so
+// each read's 16 lanes need 8 distinct slots among keys of one row parity:
+// the K swizzle makes keys n and n + 8 differ (16 keys of one chunk), the V
+// swizzle keys k and k + 16 (kappa(g, .) covers k..k+3 and k+16..k+19).
+struct F8Tile {
+  static constexpr int kCh = 8;
+  static constexpr int kRowsPerInst = 8;
+  static constexpr int kInsts = 4;
+  static constexpr int kRowBytes = 128;
+  static constexpr int kTileBytes = 2 * 32 * kRowBytes;  // K then V
+  static constexpr int kRow16 = (16 / kInsts) * kRowBytes;
+  __device__ static int row_of(int key) { return kRowsPerInst * (key % kInsts) + key / kInsts; }
+  __device__ static int kswizzle(int key) { return (key & 3) | (((key >> 3) & 1) << 2); }
+  __device__ static int vswizzle(int key) { return (key & 3) | (((key >> 4) & 1) << 2); }
+  __device__ static int offset(int key, int chunk) { return row_of(key) * kRowBytes + 16 * (chunk ^ kswizzle(key)); }
+  __device__ static int voffset(int key, int chunk) { return row_of(key) * kRowBytes + 16 * (chunk ^ vswizzle(key)); }
+};
+
+// Eight e4m3 values (bytes 0..7 of lo, hi) as an MFMA operand of bf16 or
+// fp16: every e4m3 value is exact in both. The conversions run with scale 1;
+// a pool's scales are applied to the scores and the outputs instead.
+template <typename Frag>
+__device__ __forceinline__ Frag f8x8_to_frag(uint32_t lo, uint32_t hi) {
+  u32x4_t w;
+  if constexpr (__is_same(Frag, bf16x8_t)) {
+    w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+    w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+    w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+    w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
+  } else {
+    w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false));
+    w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true));
+    w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false));
+    w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true));
+  }
+  return __builtin_bit_cast(Frag, w);
+}
+
+// The K operand of an fp8 tile: 8 bytes at LDS byte address `addr`.
+template <typename Frag>
+__device__ __forceinline__ Frag lds_read_f8_frag(uint32_t addr) {
+  typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+  const u2 v = *(const __attribute__((address_space(3))) u2*)(uintptr_t)addr;
+  return f8x8_to_frag<Frag>(v[0], v[1]);
+}
+
+// The V^T operand of an fp8 tile: one 8-bit transposing read at `addr`.
+template <typename Frag>
+__device__ __forceinline__ Frag lds_read_f8_vt(uint32_t addr) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  const v2i v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) v2i*)(uintptr_t)addr);
+  return f8x8_to_frag<Frag>((uint32_t)v[0], (uint32_t)v[1]);
+}
 
 // One direct-to-LDS load: every lane's 16 bytes at `g` land at lds + 16 * lane.
 //

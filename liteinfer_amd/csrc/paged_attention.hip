@@ -2,6 +2,8 @@
 // partition policy, and dispatch to the MFMA or the general-shape kernels.
 #include "li_attention.h"
 
+#include <cmath>
+
 #include <cstdlib>
 
 namespace li {
@@ -97,7 +99,7 @@ void set_balanced(AttnArgs& d, int waves, void* workspace) {
 }
 
 int check_common(int dtype, int num_heads, int num_kv_heads, int head_dim, const char* who) {
-  if (dtype_size(dtype) == 0) return fail(LI_EINVAL, "%s: unknown dtype %d", who, dtype);
+  if (dtype_size(dtype) == 0 || dtype == LI_FP8_E4M3) return fail(LI_EINVAL, "%s: unknown query dtype %d", who, dtype);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return fail(LI_EINVAL, "%s: %d query heads cannot be grouped over %d KV heads", who, num_heads, num_kv_heads);
   if (head_dim <= 0 || head_dim > kGenericMaxHeadDim)
@@ -147,15 +149,28 @@ extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, 
   return LI_OK;
 }
 
-extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* key_pool,
-                               const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
-                               const int64_t* slot_table, int64_t slot_table_stride, int max_context,
-                               const int32_t* context_lens, void* out, int64_t out_stride_seq,
-                               int64_t out_stride_head, int batch, int num_heads, int num_kv_heads, int head_dim,
-                               float scale, int num_splits, int block_kv, void* workspace, size_t workspace_bytes,
-                               int dtype, int flags, void* stream) {
+// The pool's element type against the query's: the same type, or fp8 (e4m3)
+// with scales, which only the MFMA kernels read.
+int check_kv(int dtype, int kv_dtype, float k_scale, float v_scale, const char* who) {
+  if (kv_dtype == dtype) return LI_OK;
+  if (kv_dtype != LI_FP8_E4M3)
+    return fail(LI_EINVAL, "%s: pool dtype %d does not match the query's %d", who, kv_dtype, dtype);
+  if (!(k_scale > 0.f) || !(v_scale > 0.f) || !std::isfinite(k_scale) || !std::isfinite(v_scale))
+    return fail(LI_EINVAL, "%s: fp8 pool scales must be finite and > 0 (k_scale=%g, v_scale=%g)", who, k_scale,
+                v_scale);
+  return LI_OK;
+}
+
+int paged_decode_impl(const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* key_pool,
+                      const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                      const int64_t* slot_table, int64_t slot_table_stride, int max_context,
+                      const int32_t* context_lens, void* out, int64_t out_stride_seq, int64_t out_stride_head,
+                      int batch, int num_heads, int num_kv_heads, int head_dim, float scale, int num_splits,
+                      int block_kv, void* workspace, size_t workspace_bytes, int dtype, int kv_dtype, float k_scale,
+                      float v_scale, int flags, void* stream) {
   clear_error();
   if (int rc = check_common(dtype, num_heads, num_kv_heads, head_dim, "li_paged_decode")) return rc;
+  if (int rc = check_kv(dtype, kv_dtype, k_scale, v_scale, "li_paged_decode")) return rc;
   if (num_splits < 0) return fail(LI_EINVAL, "num_splits must be >= 1, got %d", num_splits);
   if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_decode: negative extent");
   if (batch == 0) return LI_OK;
@@ -196,6 +211,9 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
   a.block_q = 1;
   a.block_kv = block_kv > 0 ? block_kv : kDefaultBlockKv;
   a.num_qblocks = 1;
+  a.kv_fp8 = kv_dtype == LI_FP8_E4M3;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
   if (parts > 1) {
     const size_t rows = (size_t)batch * num_heads * parts;
     a.part_o = static_cast<float*>(workspace);
@@ -204,6 +222,10 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool mfma = !(flags & LI_FLAG_FORCE_GENERIC) && decode_mfma_applies(a, dtype);
+  if (a.kv_fp8 && !mfma)
+    return fail(LI_EUNSUPPORTED,
+                "li_paged_decode: fp8 pools run on the MFMA kernel only (bf16 / fp16 queries, head_dim 128, "
+                "16-byte aligned rows)");
   if (mfma && (num_splits == 0 || !(flags & LI_FLAG_EQUAL_SPLITS))) {
     // The MFMA kernel's schedule: the balanced split (it launches its own
     // combine). A split count the caller chose (the engine passes
@@ -220,6 +242,33 @@ extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_st
   if (rc) return rc;
   if (parts > 1) rc = launch_combine(a, dtype, s);
   return rc;
+}
+
+extern "C" int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* key_pool,
+                               const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                               const int64_t* slot_table, int64_t slot_table_stride, int max_context,
+                               const int32_t* context_lens, void* out, int64_t out_stride_seq,
+                               int64_t out_stride_head, int batch, int num_heads, int num_kv_heads, int head_dim,
+                               float scale, int num_splits, int block_kv, void* workspace, size_t workspace_bytes,
+                               int dtype, int flags, void* stream) {
+  return paged_decode_impl(q, q_stride_seq, q_stride_head, key_pool, value_pool, pool_stride_slot, pool_stride_head,
+                           slot_table, slot_table_stride, max_context, context_lens, out, out_stride_seq,
+                           out_stride_head, batch, num_heads, num_kv_heads, head_dim, scale, num_splits, block_kv,
+                           workspace, workspace_bytes, dtype, dtype, 1.f, 1.f, flags, stream);
+}
+
+extern "C" int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* key_pool,
+                                  const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                                  const int64_t* slot_table, int64_t slot_table_stride, int max_context,
+                                  const int32_t* context_lens, void* out, int64_t out_stride_seq,
+                                  int64_t out_stride_head, int batch, int num_heads, int num_kv_heads, int head_dim,
+                                  float scale, int num_splits, int block_kv, void* workspace,
+                                  size_t workspace_bytes, int dtype, int kv_dtype, float k_scale, float v_scale,
+                                  int flags, void* stream) {
+  return paged_decode_impl(q, q_stride_seq, q_stride_head, key_pool, value_pool, pool_stride_slot, pool_stride_head,
+                           slot_table, slot_table_stride, max_context, context_lens, out, out_stride_seq,
+                           out_stride_head, batch, num_heads, num_kv_heads, head_dim, scale, num_splits, block_kv,
+                           workspace, workspace_bytes, dtype, kv_dtype, k_scale, v_scale, flags, stream);
 }
 
 // Workspace of the MFMA prefill path: the balanced decode kernel's partials

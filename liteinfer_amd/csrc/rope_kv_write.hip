@@ -226,6 +226,8 @@ extern "C" int li_rope_kv_write(const void* q, const int64_t* q_strides, const v
   li::clear_error();
   const int esize = li::dtype_size(dtype);
   if (esize == 0) return li::fail(LI_EINVAL, "li_rope_kv_write: unknown dtype %d", dtype);
+  if (dtype == LI_FP8_E4M3)
+    return li::fail(LI_EUNSUPPORTED, "li_rope_kv_write: fp8 pools are written by li_kv_scatter_fp8 (quantising), not copied");
   if (batch < 0 || tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_slots < 0)
     return li::fail(LI_EINVAL, "li_rope_kv_write: negative or empty extent");
   if (head_dim % 2 != 0) return li::fail(LI_EINVAL, "li_rope_kv_write: head_dim %d is odd", head_dim);

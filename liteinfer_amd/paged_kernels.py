@@ -121,6 +121,18 @@ def _check_pools(key_pool: torch.Tensor, value_pool: torch.Tensor) -> None:
         raise ValueError("key and value pools must share a dtype")
 
 
+def _kv_dtype_code(query: torch.Tensor, key_pool: torch.Tensor, k_scale: float, v_scale: float) -> int:
+    """The pool's element type code: the query's, or fp8 (with checked scales)."""
+    if _is_fp8(key_pool):
+        if query.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"an fp8 pool is read with bfloat16 or float16 queries, not {query.dtype}")
+        _check_scales(k_scale, v_scale)
+        return _native.LI_FP8_E4M3
+    if query.dtype != key_pool.dtype:
+        raise ValueError(f"query dtype {query.dtype} does not match the pool's {key_pool.dtype}")
+    return _native.dtype_code(query.dtype)
+
+
 def _as_index(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return t if t.dtype == dtype else t.to(dtype)
 
@@ -129,19 +141,35 @@ def _last_dim_contiguous(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _is_fp8(pool: torch.Tensor) -> bool:
+    return pool.dtype == _native.FP8_POOL_DTYPE
+
+
+def _check_scales(k_scale: float, v_scale: float) -> None:
+    for name, value in (("k_scale", k_scale), ("v_scale", v_scale)):
+        if not (value > 0 and value != float("inf")):
+            raise ValueError(f"{name} must be finite and > 0, got {value}")
+
+
 def kv_scatter(
     key_pool: torch.Tensor,
     value_pool: torch.Tensor,
     slots: torch.Tensor,
     k: torch.Tensor,
     v: torch.Tensor,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> None:
     """Store one K/V column per slot, in the order the pass holds its tokens.
 
     `k` and `v` are ``[B, H, T, D]`` (any strides); `slots` holds ``B * T``
     entries taken batch-major, ``[1, T]`` for a packed pass or ``[1, B]`` for a
     decode step (kv_cache.py:236-247). The pools are this layer's
-    ``[num_slots, H, D]`` stores and are written in place, bit for bit.
+    ``[num_slots, H, D]`` stores and are written in place, bit for bit — or,
+    for an fp8 (``torch.float8_e4m3fn``) pool, each element quantised as
+    ``e4m3(clamp(x * (1 / scale), +-448))`` with ``k_scale`` / ``v_scale``
+    (the reference's planned storage-level quantisation, roadmap section 2.5).
     """
     device = _require_device_tensors(key_pool, value_pool, slots, k, v)
     _check_pools(key_pool, value_pool)
@@ -150,12 +178,29 @@ def kv_scatter(
     batch, heads, tokens, head_dim = k.shape
     if heads != key_pool.shape[1] or head_dim != key_pool.shape[2]:
         raise ValueError(f"k rows {heads}x{head_dim} do not match the pool's {tuple(key_pool.shape[1:])}")
-    if k.dtype != key_pool.dtype or v.dtype != key_pool.dtype:
+    fp8 = _is_fp8(key_pool)
+    if fp8:
+        if k.dtype != v.dtype or k.dtype not in _native.DTYPE_CODES:
+            raise ValueError(f"an fp8 pool takes float32 / float16 / bfloat16 k and v, got {k.dtype}, {v.dtype}")
+        _check_scales(k_scale, v_scale)
+    elif k.dtype != key_pool.dtype or v.dtype != key_pool.dtype:
         raise ValueError(f"k/v dtype {k.dtype} does not match the pool's {key_pool.dtype}")
     flat_slots = _as_index(slots.reshape(-1), torch.int64).contiguous()
     if flat_slots.numel() != batch * tokens:
         raise ValueError(f"{flat_slots.numel()} slots for {batch * tokens} tokens")
     lib = _native.load()
+    if fp8:
+        status = lib.li_kv_scatter_fp8(
+            k.data_ptr(), v.data_ptr(),
+            _native.i64_array(k.stride()), _native.i64_array(v.stride()),
+            batch, tokens, flat_slots.data_ptr(),
+            key_pool.data_ptr(), value_pool.data_ptr(),
+            key_pool.shape[0], key_pool.stride(0), key_pool.stride(1),
+            heads, head_dim, _native.dtype_code(k.dtype), float(k_scale), float(v_scale),
+            _native.stream_handle(device),
+        )
+        _native.check(status, "kv_scatter")
+        return
     status = lib.li_kv_scatter(
         k.data_ptr(), v.data_ptr(),
         _native.i64_array(k.stride()), _native.i64_array(v.stride()),
@@ -180,6 +225,8 @@ def paged_decode(
     num_splits: int | None = None,
     *,
     kernel: str = "auto",
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Attend one query per sequence over the KV each sequence's slots address.
 
@@ -204,6 +251,10 @@ def paged_decode(
             way, within fp32 rounding of the partial combine.
         kernel: ``"auto"`` (MFMA where it applies), ``"generic"`` (the
             general-shape kernel) or ``"equal_splits"`` (MFMA, splits pinned).
+        k_scale, v_scale: the scales of an fp8 (``torch.float8_e4m3fn``) pool,
+            whose rows hold K / k_scale and V / v_scale (`kv_scatter`); the
+            attention is over the dequantised rows. fp8 pools run on the MFMA
+            kernel (bf16 / fp16 queries, head_dim 128). Ignored otherwise.
 
     Returns:
         ``[batch, num_heads, head_dim]``, same dtype as ``query``.
@@ -215,8 +266,7 @@ def paged_decode(
     device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens)
     _check_pools(key_pool, value_pool)
     batch, num_heads, head_dim = query.shape
-    if query.dtype != key_pool.dtype:
-        raise ValueError(f"query dtype {query.dtype} does not match the pool's {key_pool.dtype}")
+    kv_code = _kv_dtype_code(query, key_pool, k_scale, v_scale)
     if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:
         raise ValueError(
             f"{num_heads} query heads in groups of {num_kv_groups} do not match {key_pool.shape[1]} KV heads"
@@ -242,7 +292,7 @@ def paged_decode(
 
     out = torch.empty_like(query)
     workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
-    status = lib.li_paged_decode(
+    status = lib.li_paged_decode_ex(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
         slot_table.data_ptr(), slot_table.stride(0), max_context,
@@ -250,7 +300,8 @@ def paged_decode(
         batch, num_heads, num_kv_heads, head_dim, float(scaling),
         num_splits or 0, block_kv,
         workspace.data_ptr() if workspace is not None else None, need.value,
-        _native.dtype_code(query.dtype), _flags(kernel), _native.stream_handle(device),
+        _native.dtype_code(query.dtype), kv_code, float(k_scale), float(v_scale),
+        _flags(kernel), _native.stream_handle(device),
     )
     _native.check(status, "paged_decode")
     return out

@@ -1,0 +1,138 @@
+"""The fp8 (e4m3) KV pool on the GPU: quantising slot-write and dequantising decode.
+
+The slot-write is bit-exact against the oracle's quantiser (oracle/fp8.py,
+pinned against torch's float8_e4m3fn). Attention over an fp8 pool is held to
+the bf16 bar (max-abs 2e-2, mean-abs 2e-3) against the fp64 oracle over the
+same dequantised rows; beside that, how far the quantised cache moves the
+answer from the bf16 cache on the same unquantised K/V is bounded (the
+reference's planned "tolerance parity test against fp16/bf16",
+docs/roadmap.md section 2.5).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from liteinfer_amd.paged_kernels import kv_scatter, paged_decode
+from oracle import fp8
+from oracle.attention import attend
+from tests.helpers import PagedBatch, assert_within, to_numpy
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+FP8 = torch.float8_e4m3fn
+
+
+def _codes(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+def _to_pool(codes: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(codes)).to(DEV).view(FP8)
+
+
+@pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("layout", ["bhtd", "bthd", "strided_dim"])
+@pytest.mark.parametrize(("k_scale", "v_scale"), [(1.0, 1.0), (0.25, 3.0)])
+def test_quantising_slot_write_is_bit_exact(src_dtype, layout, k_scale, v_scale):
+    g = torch.Generator(device=DEV).manual_seed(3)
+    batch, heads, tokens, dim, num_slots = 3, 8, 5, 128, 97
+    shape = (batch, tokens, heads, dim) if layout == "bthd" else (batch, heads, tokens, dim)
+    k = (torch.randn(shape, generator=g, device=DEV) * 30).to(src_dtype)   # some values saturate
+    v = (torch.randn(shape, generator=g, device=DEV) * 30).to(src_dtype)
+    if layout == "bthd":
+        k, v = k.transpose(1, 2), v.transpose(1, 2)
+    if layout == "strided_dim":
+        k = torch.cat([k, k], dim=3)[..., ::2]
+        v = torch.cat([v, v], dim=3)[..., ::2]
+    before = torch.randint(0, 255, (num_slots, heads, dim), generator=g, device=DEV, dtype=torch.uint8)
+    before[before == 0x7F] = 0  # no NaN codes, so equality below is plain
+    kp, vp = before.clone().view(FP8), before.clone().view(FP8)
+    slots = torch.tensor([[5, 96, 0, 41, 17, 8, 60, 3, 77, 12, 30, 90, 2, 55, -1]], device=DEV)
+    slots[0, -1] = 1000  # out of range: skipped
+    kv_scatter(kp, vp, slots, k, v, k_scale=k_scale, v_scale=v_scale)
+
+    want_k, want_v = _codes(before), _codes(before)
+    kf = to_numpy(k).astype(np.float32)
+    vf = to_numpy(v).astype(np.float32)
+    for i, s in enumerate(slots[0].tolist()):
+        if not 0 <= s < num_slots:
+            continue
+        b, t = divmod(i, tokens)
+        want_k[s] = fp8.quantize(kf[b, :, t, :], k_scale)
+        want_v[s] = fp8.quantize(vf[b, :, t, :], v_scale)
+    assert np.array_equal(_codes(kp), want_k)
+    assert np.array_equal(_codes(vp), want_v)
+
+
+def _fp8_batch(context_lens, k_scale, v_scale, q_dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, seed=0,
+               num_slots=65536):
+    """A decode batch whose pools are quantised by the oracle; returns it, the fp8 pools and the fp64 oracle."""
+    b = PagedBatch(context_lens, dtype=q_dtype, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=128,
+                   num_slots=num_slots, seed=seed)
+    kc = fp8.quantize(to_numpy(b.key_pool), k_scale)
+    vc = fp8.quantize(to_numpy(b.value_pool), v_scale)
+    kd, vd = fp8.dequantize(kc, k_scale), fp8.dequantize(vc, v_scale)
+    want = attend(to_numpy(b.query), kd, vd, b.slot_table.cpu().numpy(), np.asarray(context_lens), b.scaling,
+                  b.groups, dtype=np.float64)
+    return b, _to_pool(kc), _to_pool(vc), want
+
+
+@pytest.mark.parametrize("kernel", ["auto", "equal_splits"])
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("k_scale", "v_scale"), [(1.0, 1.0), (0.05, 0.2)])
+def test_fp8_decode_matches_the_oracle_over_dequantised_rows(kernel, q_dtype, k_scale, v_scale):
+    ctx = [1, 31, 32, 33, 500, 1023, 2100, 4096]
+    b, kp, vp, want = _fp8_batch(ctx, k_scale, v_scale, q_dtype=q_dtype, seed=4)
+    out = paged_decode(b.query, kp, vp, b.slot_table, b.context_lens_t, b.scaling, b.groups, num_splits=4,
+                       kernel=kernel, k_scale=k_scale, v_scale=v_scale)
+    assert_within(out, want / 1.0, 2e-2, 2e-3)
+
+
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (8, 8), (16, 1), (20, 4)])
+def test_fp8_decode_groupings(num_heads, num_kv_heads):
+    b, kp, vp, want = _fp8_batch([7, 300, 1500], 0.5, 0.5, num_heads=num_heads, num_kv_heads=num_kv_heads, seed=5,
+                                 num_slots=8192)
+    out = paged_decode(b.query, kp, vp, b.slot_table, b.context_lens_t, b.scaling, b.groups, k_scale=0.5,
+                       v_scale=0.5)
+    assert_within(out, want, 2e-2, 2e-3)
+
+
+def test_c2_fp8_pool_full_size_and_against_the_bf16_cache():
+    """Config 2's decode step on an fp8 pool: at the bf16 bar against the oracle over the
+    dequantised rows, and within a bounded distance of the same step on the bf16 pool."""
+    from liteinfer_amd.workloads import decode_step
+
+    step = decode_step("c2", seed=0)
+    kp = torch.empty(step.key_pool.shape, dtype=FP8, device=DEV)
+    vp = torch.empty_like(kp)
+    all_slots = torch.arange(kp.shape[0], device=DEV).view(1, -1)
+    kv_scatter(kp, vp, all_slots, step.key_pool.unsqueeze(0).transpose(1, 2),
+               step.value_pool.unsqueeze(0).transpose(1, 2))
+    g = step.geometry
+    out8 = paged_decode(step.query, kp, vp, step.slot_table, step.context_lens, g.scaling, g.groups)
+    out16 = paged_decode(step.query, step.key_pool, step.value_pool, step.slot_table, step.context_lens,
+                         g.scaling, g.groups)
+    kd = fp8.dequantize(_codes(kp), 1.0)
+    vd = fp8.dequantize(_codes(vp), 1.0)
+    want = attend(to_numpy(step.query), kd, vd, step.slot_table.cpu().numpy(),
+                  np.asarray(step.host_context_lens), g.scaling, g.groups, dtype=np.float32)
+    assert_within(out8, want, 2e-2, 2e-3)
+    diff = (out8.float() - out16.float()).abs()
+    assert diff.max().item() <= 2e-2 and diff.mean().item() <= 2e-3, (diff.max().item(), diff.mean().item())
+
+
+def test_fp8_pool_rejects_what_it_cannot_serve():
+    b = PagedBatch([40], dtype=torch.float32, num_heads=8, num_kv_heads=2, head_dim=128, num_slots=256)
+    kp = torch.zeros(256, 2, 128, dtype=FP8, device=DEV)
+    with pytest.raises(ValueError, match="bfloat16 or float16"):
+        paged_decode(b.query, kp, kp.clone(), b.slot_table, b.context_lens_t, b.scaling, b.groups)
+    q = b.query.to(torch.bfloat16)
+    with pytest.raises(ValueError, match="k_scale"):
+        paged_decode(q, kp, kp.clone(), b.slot_table, b.context_lens_t, b.scaling, b.groups, k_scale=0.0)
+    kp64 = torch.zeros(256, 2, 64, dtype=FP8, device=DEV)
+    b64 = PagedBatch([40], dtype=torch.bfloat16, num_heads=8, num_kv_heads=2, head_dim=64, num_slots=256)
+    with pytest.raises(ValueError, match="MFMA kernel only"):
+        paged_decode(b64.query, kp64, kp64.clone(), b64.slot_table, b64.context_lens_t, b64.scaling, b64.groups)
