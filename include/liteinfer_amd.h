@@ -240,6 +240,26 @@ int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                      void* workspace, size_t workspace_bytes, int dtype,
                      int flags, void* stream);
 
+/*
+ * li_paged_prefill over a pool of element type kv_dtype: `dtype` (then the
+ * scales are ignored and this is li_paged_prefill) or LI_FP8_E4M3, as for
+ * li_paged_decode_ex (its one-query sequences run on li_paged_decode_ex's
+ * kernel). fp8 pools run on the MFMA kernels only (bf16 / fp16 queries,
+ * head_dim 128; otherwise LI_EUNSUPPORTED). No counterpart in the
+ * reference's code (its planned quantised cache, docs/roadmap.md 2.5).
+ */
+int li_paged_prefill_ex(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const void* key_pool, const void* value_pool,
+                        int64_t pool_stride_slot, int64_t pool_stride_head,
+                        const int64_t* slot_table, int64_t slot_table_stride,
+                        int max_context, const int32_t* context_lens,
+                        const int32_t* query_start_loc, int batch, int max_query_len,
+                        void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                        int num_heads, int num_kv_heads, int head_dim, float scale,
+                        int block_q, int block_kv, void* workspace,
+                        size_t workspace_bytes, int dtype, int kv_dtype,
+                        float k_scale, float v_scale, int flags, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "li_paged_decode_ex",
     "li_paged_prefill_plan",
     "li_paged_prefill",
+    "li_paged_prefill_ex",
 )
 
 _i64, _i32, _p, _f32, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
@@ -83,6 +84,11 @@ _SIGNATURES = {
         _i32,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _i64,
          _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _p],
+    ),
+    "li_paged_prefill_ex": (
+        _i32,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _i64,
+         _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _f32, _f32, _i32, _p],
     ),
 }
 

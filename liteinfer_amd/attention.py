@@ -48,6 +48,10 @@ class PagedKV(NamedTuple):
     """`context_lens` on the host, for the dense kernels' per-sequence slicing."""
     host_query_lens: tuple[int, ...] = ()
     """Each sequence's query count on the host, for the same slicing."""
+    k_scale: float = 1.0
+    """An fp8 (``torch.float8_e4m3fn``) pool holds K / k_scale; unused otherwise."""
+    v_scale: float = 1.0
+    """An fp8 pool holds V / v_scale; unused otherwise."""
 
 
 # ---------------------------------------------------------------------------
@@ -69,9 +73,16 @@ def _causal_visibility(num_queries: int, num_keys: int, device: torch.device) ->
     return key_pos[None, :] <= query_pos[:, None]
 
 
-def _gather(pool: torch.Tensor, slots: torch.Tensor) -> torch.Tensor:
-    """``[B, W]`` slots of a ``[S, Hkv, D]`` pool -> ``[B, Hkv, W, D]``."""
-    return pool[slots].transpose(1, 2)
+def _gather(pool: torch.Tensor, slots: torch.Tensor, like: torch.Tensor, scale: float) -> torch.Tensor:
+    """``[B, W]`` slots of a ``[S, Hkv, D]`` pool -> ``[B, Hkv, W, D]`` in `like`'s dtype.
+
+    An fp8 pool's rows are dequantised (times `scale`) in float32, then
+    rounded to the query's dtype, the values the dense arithmetic then uses.
+    """
+    rows = pool[slots].transpose(1, 2)
+    if rows.dtype == torch.float8_e4m3fn:
+        rows = (rows.to(torch.float32) * scale).to(like.dtype)
+    return rows
 
 
 # (query, keys, values, visible-or-None, is_causal) -> output
@@ -112,8 +123,8 @@ def _dense_decode(query: torch.Tensor, kv: PagedKV, attend: _Attend) -> torch.Te
     """Every row's context gathered at once, each bounded by its own length."""
     width = kv.slot_table.shape[1]
     bound = torch.arange(width, device=query.device)[None, :] < kv.context_lens.to(query.device)[:, None]
-    keys = _gather(kv.key_pool, kv.slot_table)
-    values = _gather(kv.value_pool, kv.slot_table)
+    keys = _gather(kv.key_pool, kv.slot_table, query, kv.k_scale)
+    values = _gather(kv.value_pool, kv.slot_table, query, kv.v_scale)
     return attend(query, keys, values, bound[:, None, None, :], False)
 
 
@@ -132,7 +143,9 @@ def _dense_packed(query: torch.Tensor, kv: PagedKV, attend: _Attend) -> torch.Te
         whole_prompt = nq == ctx
         is_causal = nq > 1 and whole_prompt
         visible = _causal_visibility(nq, ctx, query.device) if (nq > 1 and not whole_prompt) else None
-        pieces.append(attend(chunk, _gather(kv.key_pool, slots), _gather(kv.value_pool, slots), visible, is_causal))
+        keys = _gather(kv.key_pool, slots, chunk, kv.k_scale)
+        values = _gather(kv.value_pool, slots, chunk, kv.v_scale)
+        pieces.append(attend(chunk, keys, values, visible, is_causal))
     return torch.cat(pieces, dim=2)
 
 
@@ -166,7 +179,7 @@ def _paged_decode_step(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_
 
     out = paged_decode(
         query.squeeze(2), kv.key_pool, kv.value_pool, kv.slot_table, kv.context_lens,
-        scaling, num_kv_groups, num_splits=kv.num_splits,
+        scaling, num_kv_groups, num_splits=kv.num_splits, k_scale=kv.k_scale, v_scale=kv.v_scale,
     )
     return out.unsqueeze(2)
 
@@ -181,6 +194,7 @@ def _paged_packed(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_group
     out = paged_prefill(
         query.squeeze(0).transpose(0, 1), kv.key_pool, kv.value_pool, kv.slot_table, kv.context_lens,
         kv.query_start_loc, kv.max_query_len, scaling, num_kv_groups, one_query_rows=one_query_rows,
+        k_scale=kv.k_scale, v_scale=kv.v_scale,
     )
     return out.transpose(0, 1).unsqueeze(0)
 

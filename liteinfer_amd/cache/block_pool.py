@@ -27,8 +27,18 @@ class BlockPoolExhaustedError(RuntimeError):
     """The pool cannot hold what was asked of it."""
 
 
+CACHE_QUANT_FORMATS = (None, "fp8")
+
+
 class BlockPool:
-    """Fixed-size pool of KV blocks shared by all layers, with one free-list."""
+    """Fixed-size pool of KV blocks shared by all layers, with one free-list.
+
+    ``cache_quant="fp8"`` stores K and V as OCP e4m3 (``torch.float8_e4m3fn``),
+    one byte per element: each row is written as ``x / k_scale`` (``v_scale``
+    for V) rounded to e4m3 and read back times the scale — the reference's
+    planned storage-level quantisation (docs/roadmap.md section 2.5, behind a
+    ``cache_quant`` flag). ``dtype`` stays the dtype K/V arrive and leave in.
+    """
 
     def __init__(
         self,
@@ -39,15 +49,27 @@ class BlockPool:
         head_dim: int,
         dtype: torch.dtype,
         device: torch.device,
+        cache_quant: str | None = None,
+        k_scale: float = 1.0,
+        v_scale: float = 1.0,
     ) -> None:
+        if cache_quant not in CACHE_QUANT_FORMATS:
+            raise ValueError(f"cache_quant must be one of {CACHE_QUANT_FORMATS}, got {cache_quant!r}")
+        if not (k_scale > 0 and v_scale > 0):
+            raise ValueError(f"k_scale and v_scale must be > 0, got {k_scale}, {v_scale}")
         self.num_blocks = num_blocks
         self.block_size = block_size
         self.num_layers = num_layers
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
+        self.dtype = dtype
+        self.cache_quant = cache_quant
+        self.k_scale = float(k_scale)
+        self.v_scale = float(v_scale)
+        storage = torch.float8_e4m3fn if cache_quant == "fp8" else dtype
         shape = (num_layers, num_blocks * block_size, num_kv_heads, head_dim)
-        self._keys = torch.zeros(shape, dtype=dtype, device=device)
-        self._values = torch.zeros(shape, dtype=dtype, device=device)
+        self._keys = torch.zeros(shape, dtype=storage, device=device)
+        self._values = torch.zeros(shape, dtype=storage, device=device)
         self._free_blocks: list[int] = list(range(num_blocks))
 
     @property

@@ -41,15 +41,28 @@ def tokens_first(states: torch.Tensor) -> torch.Tensor:
     return states.transpose(1, 2).reshape(batch * tokens, heads, dim)
 
 
+def quantize_fp8(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """Rows as an fp8 pool stores them: ``e4m3(clamp(float32(x) * float32(1 / scale), +-448))``."""
+    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(scale, dtype=torch.float32)
+    return (x.to(torch.float32) * inv.to(x.device)).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+
+
 def scatter_into(key_pool: torch.Tensor, value_pool: torch.Tensor, slots: torch.Tensor,
-                 k: torch.Tensor, v: torch.Tensor) -> None:
-    """Store ``[B, H, T, D]`` K/V rows at `slots` (B*T entries, batch-major) of one layer's pools."""
+                 k: torch.Tensor, v: torch.Tensor, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
+    """Store ``[B, H, T, D]`` K/V rows at `slots` (B*T entries, batch-major) of one layer's pools.
+
+    An fp8 pool stores each row quantised with its scale (`quantize_fp8`).
+    """
     if key_pool.device.type == "cuda":
         from liteinfer_amd.paged_kernels import kv_scatter
 
-        kv_scatter(key_pool, value_pool, slots, k, v)
+        kv_scatter(key_pool, value_pool, slots, k, v, k_scale=k_scale, v_scale=v_scale)
         return
     flat = slots.reshape(-1)
+    if key_pool.dtype == torch.float8_e4m3fn:
+        key_pool[flat] = quantize_fp8(tokens_first(k), k_scale)
+        value_pool[flat] = quantize_fp8(tokens_first(v), v_scale)
+        return
     key_pool[flat] = tokens_first(k)
     value_pool[flat] = tokens_first(v)
 
@@ -126,7 +139,7 @@ class KVCache:
     def scatter(self, layer_idx: int, slots: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         """Store one K/V column per slot, in the order the pass holds its tokens (kv_cache.py:236-247)."""
         keys, values = self._pool.slots(layer_idx)
-        scatter_into(keys, values, slots, k, v)
+        scatter_into(keys, values, slots, k, v, self._pool.k_scale, self._pool.v_scale)
 
     def rotate_and_scatter(self, layer_idx: int, slots: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
                            v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -136,14 +149,14 @@ class KVCache:
         of llama.py:85-98 and `scatter` on the CPU.
         """
         keys, values = self._pool.slots(layer_idx)
-        if keys.device.type == "cuda":
+        if keys.device.type == "cuda" and self._pool.cache_quant is None:
             from liteinfer_amd.rope import rope_kv_write
 
             return rope_kv_write(q, k, v, cos, sin, slots, keys, values)
         from liteinfer_amd.rope import apply_rotary_pos_emb
 
         q_embed, k_embed = apply_rotary_pos_emb(q, k, cos, sin)
-        scatter_into(keys, values, slots, k_embed, v)
+        scatter_into(keys, values, slots, k_embed, v, self._pool.k_scale, self._pool.v_scale)
         return q_embed
 
 
@@ -180,6 +193,8 @@ class _PackedPayload:
             max_query_len=self._max_query_len,
             host_context_lens=self._host_context_lens,
             host_query_lens=self._host_query_lens,
+            k_scale=self._cache.pool.k_scale,
+            v_scale=self._cache.pool.v_scale,
         )
 
 
@@ -207,4 +222,6 @@ class _DecodePayload:
 
     def _paged_kv(self, layer_idx: int) -> PagedKV:
         key_pool, value_pool = self._cache.layer_storage(layer_idx)
-        return PagedKV(key_pool, value_pool, self._slots, self._context_lens, self._num_splits)
+        pool = self._cache.pool
+        return PagedKV(key_pool, value_pool, self._slots, self._context_lens, self._num_splits,
+                       k_scale=pool.k_scale, v_scale=pool.v_scale)

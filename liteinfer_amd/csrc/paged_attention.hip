@@ -290,16 +290,16 @@ extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
   return LI_OK;
 }
 
-extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool,
-                                const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
-                                const int64_t* slot_table, int64_t slot_table_stride, int max_context,
-                                const int32_t* context_lens, const int32_t* query_start_loc, int batch,
-                                int max_query_len, void* out, int64_t out_stride_tok, int64_t out_stride_head,
-                                int num_heads, int num_kv_heads, int head_dim, float scale, int block_q,
-                                int block_kv, void* workspace, size_t workspace_bytes, int dtype, int flags,
-                                void* stream) {
+int paged_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool,
+                       const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                       const int64_t* slot_table, int64_t slot_table_stride, int max_context,
+                       const int32_t* context_lens, const int32_t* query_start_loc, int batch, int max_query_len,
+                       void* out, int64_t out_stride_tok, int64_t out_stride_head, int num_heads, int num_kv_heads,
+                       int head_dim, float scale, int block_q, int block_kv, void* workspace, size_t workspace_bytes,
+                       int dtype, int kv_dtype, float k_scale, float v_scale, int flags, void* stream) {
   clear_error();
   if (int rc = check_common(dtype, num_heads, num_kv_heads, head_dim, "li_paged_prefill")) return rc;
+  if (int rc = check_kv(dtype, kv_dtype, k_scale, v_scale, "li_paged_prefill")) return rc;
   if (batch < 0 || max_query_len < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_prefill: negative extent");
   if (batch == 0 || max_query_len == 0) return LI_OK;
   if (!q || !key_pool || !value_pool || !slot_table || !context_lens || !query_start_loc || !out)
@@ -331,9 +331,17 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
   a.block_kv = block_kv > 0 ? block_kv : kDefaultBlockKv;
   a.max_query_len = max_query_len;
   a.max_context = max_context;
+  a.kv_fp8 = kv_dtype == LI_FP8_E4M3;
+  a.k_scale = k_scale;
+  a.v_scale = v_scale;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (!(flags & LI_FLAG_FORCE_GENERIC) && prefill_mfma_applies(a, dtype)) {
+  const bool mfma = !(flags & LI_FLAG_FORCE_GENERIC) && prefill_mfma_applies(a, dtype);
+  if (a.kv_fp8 && !mfma)
+    return fail(LI_EUNSUPPORTED,
+                "li_paged_prefill: fp8 pools run on the MFMA kernels only (bf16 / fp16 queries, head_dim 128, "
+                "16-byte aligned rows)");
+  if (mfma) {
     // One-query sequences (decode rows beside chunks) would leave all but G
     // of a prefill unit's 256 rows idle and walk their whole context in one
     // work-group; the decode kernel serves them instead, its key axis cut
@@ -360,4 +368,34 @@ extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_s
   a.block_q = block_q > 0 ? block_q : 16;
   a.num_qblocks = cdiv(max_query_len, a.block_q);
   return launch_attend_generic(a, dtype, s);
+}
+
+extern "C" int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool,
+                                const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                                const int64_t* slot_table, int64_t slot_table_stride, int max_context,
+                                const int32_t* context_lens, const int32_t* query_start_loc, int batch,
+                                int max_query_len, void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                                int num_heads, int num_kv_heads, int head_dim, float scale, int block_q,
+                                int block_kv, void* workspace, size_t workspace_bytes, int dtype, int flags,
+                                void* stream) {
+  return paged_prefill_impl(q, q_stride_tok, q_stride_head, key_pool, value_pool, pool_stride_slot, pool_stride_head,
+                            slot_table, slot_table_stride, max_context, context_lens, query_start_loc, batch,
+                            max_query_len, out, out_stride_tok, out_stride_head, num_heads, num_kv_heads, head_dim,
+                            scale, block_q, block_kv, workspace, workspace_bytes, dtype, dtype, 1.f, 1.f, flags,
+                            stream);
+}
+
+extern "C" int li_paged_prefill_ex(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool,
+                                   const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
+                                   const int64_t* slot_table, int64_t slot_table_stride, int max_context,
+                                   const int32_t* context_lens, const int32_t* query_start_loc, int batch,
+                                   int max_query_len, void* out, int64_t out_stride_tok, int64_t out_stride_head,
+                                   int num_heads, int num_kv_heads, int head_dim, float scale, int block_q,
+                                   int block_kv, void* workspace, size_t workspace_bytes, int dtype, int kv_dtype,
+                                   float k_scale, float v_scale, int flags, void* stream) {
+  return paged_prefill_impl(q, q_stride_tok, q_stride_head, key_pool, value_pool, pool_stride_slot, pool_stride_head,
+                            slot_table, slot_table_stride, max_context, context_lens, query_start_loc, batch,
+                            max_query_len, out, out_stride_tok, out_stride_head, num_heads, num_kv_heads, head_dim,
+                            scale, block_q, block_kv, workspace, workspace_bytes, dtype, kv_dtype, k_scale, v_scale,
+                            flags, stream);
 }

@@ -63,10 +63,10 @@ constexpr int kStageKeys = 64;
 // instructions each for K and V (kInsts per 32-key half); wave w issues
 // pairs p = w * kPer .. w * kPer + kPer - 1, pair p being instruction
 // p % kInsts of half p / kInsts.
-template <typename T, int D, int W>
-__device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ kpool, const T* __restrict__ vpool,
-                                            const int* __restrict__ sl, uint32_t row_bytes, int t, int lane, int w) {
-  using L = TileLayout<D>;
+template <typename L, int W>
+__device__ __forceinline__ void issue_stage(char* stage, const char* __restrict__ kpool,
+                                            const char* __restrict__ vpool, const int* __restrict__ sl,
+                                            uint32_t row_bytes, int t, int lane, int w) {
   constexpr int kPer = 2 * L::kInsts / W;
   static_assert(kPer >= 1 && kPer * W == 2 * L::kInsts, "waves must split the stage's loads evenly");
   const int rr = lane / L::kCh, nn = lane % L::kCh;
@@ -84,23 +84,52 @@ __device__ __forceinline__ void issue_stage(char* stage, const T* __restrict__ k
     const int key = rr * L::kInsts + i;
     const uint32_t dst = lds_addr(stage + half * L::kTileBytes + i * 1024);
     // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
-    dma16(row_ptr(kpool + 8 * (nn ^ (key % L::kCh)), slot[ii], row_bytes), dst);
-    dma16(row_ptr(vpool + 8 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), dst + 32 * L::kRowBytes);
+    dma16(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), slot[ii], row_bytes), dst);
+    dma16(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), dst + 32 * L::kRowBytes);
   }
 }
 
-template <typename T, int D, int W>
+// An fp8 stage (raw, F8Tile layout, two 32-key tiles) into the 16-bit stage
+// the fold reads (TileLayout<128>): each 16-byte chunk of 16 e4m3 values of
+// a key becomes its two 16-byte chunks of bf16 / fp16, K and V rows with
+// their own swizzles. Every thread of the work-group converts its share, so
+// each value is converted once for all the waves that fold it.
+template <typename T, int W>
+__device__ __forceinline__ void convert_stage(uint32_t raw, uint32_t dst, int tid) {
+  using Frag = typename Mfma<T>::Frag;
+  using L = TileLayout<128>;
+  typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+  for (int u = tid; u < 1024; u += 64 * W) {
+    const int tile = u >> 9, kv = (u >> 8) & 1, key = (u >> 3) & 31, c8 = u & 7;
+    const uint32_t src = raw + tile * F8Tile::kTileBytes + kv * 32 * F8Tile::kRowBytes +
+                         (kv ? F8Tile::voffset(key, c8) : F8Tile::offset(key, c8));
+    const u4 x = *(const __attribute__((address_space(3))) u4*)(uintptr_t)src;
+    const uint32_t d = dst + tile * L::kTileBytes + kv * 32 * L::kRowBytes;
+    const uint32_t lo = d + (kv ? L::voffset(key, 2 * c8) : L::offset(key, 2 * c8));
+    const uint32_t hi = d + (kv ? L::voffset(key, 2 * c8 + 1) : L::offset(key, 2 * c8 + 1));
+    *(__attribute__((address_space(3))) Frag*)(uintptr_t)lo = f8x8_to_frag<Frag>(x[0], x[1]);
+    *(__attribute__((address_space(3))) Frag*)(uintptr_t)hi = f8x8_to_frag<Frag>(x[2], x[3]);
+  }
+}
+
+// F8: the pool is fp8 (e4m3, head_dim 128); its stages land raw and are
+// converted in LDS (convert_stage) before the fold, which is the same.
+template <typename T, int D, int W, bool F8>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma(AttnArgs a) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
   using L = TileLayout<D>;
+  using LS = std::conditional_t<F8, F8Tile, TileLayout<D>>;  // layout the loads fill
+  static_assert(!F8 || D == 128, "fp8 pools at head_dim 128");
   constexpr int kSteps = D / 32;
-  constexpr int kDmaPerStage = 2 * (2 * L::kInsts / W);
+  constexpr int kDmaPerStage = 2 * (2 * LS::kInsts / W);
   // Keys whose slots are staged in LDS at a time (restaging costs a pipeline
   // drain, so chunks are long).
   constexpr int kChunk = 4096;
   __shared__ __attribute__((aligned(16))) int sl[kChunk + kStageKeys];
   __shared__ __attribute__((aligned(1024))) char stages[2][2 * L::kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char raw[F8 ? 2 : 1][F8 ? 2 * F8Tile::kTileBytes : 16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -175,11 +204,14 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   // other wave there.
   const bool idle = 32 * w >= (q1 - q0) * G;
 
-  const T* kpool = static_cast<const T*>(a.kp) + (int64_t)kvh * a.p_s1;
-  const T* vpool = static_cast<const T*>(a.vp) + (int64_t)kvh * a.p_s1;
+  const int esize = F8 ? 1 : (int)sizeof(T);  // bytes per pool element
+  const char* kpool = static_cast<const char*>(a.kp) + (int64_t)kvh * a.p_s1 * esize;
+  const char* vpool = static_cast<const char*>(a.vp) + (int64_t)kvh * a.p_s1 * esize;
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
-  const uint32_t row_bytes = (uint32_t)(a.p_s0 * sizeof(T));
-  const float sc = a.scale * kLog2eMfma;
+  const uint32_t row_bytes = (uint32_t)(a.p_s0 * esize);
+  // An fp8 pool stores K / k_scale and V / v_scale: the scales multiply the
+  // scores and the outputs.
+  const float sc = a.scale * (F8 ? a.k_scale : 1.f) * kLog2eMfma;
 
   // acc[nb][blk] for blk < D / 16: dims 16 blk + 4g .. of the lane's row;
   // acc[nb][D / 16]: the row's softmax denominator, as the MFMA product of
@@ -321,19 +353,43 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // Past the chunk the look-ahead re-reads a real stage (cache hits), so
     // every wave has the same loads in flight at every wait. The loop body
     // handles both stages so that each stage's LDS offsets are constants.
-    issue_stage<T, D, W>(stages[0], kpool, vpool, sl, row_bytes, 0, lane, w);
-    for (int ti = 0; ti < ntiles; ti += 2) {
-      issue_stage<T, D, W>(stages[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
-      li_wait_vm<kDmaPerStage>();
-      __syncthreads();
-      if (!idle) fold(Stage0{}, c0 + kStageKeys * ti);
-      __syncthreads();
-      if (ti + 1 >= ntiles) break;
-      issue_stage<T, D, W>(stages[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
-      li_wait_vm<kDmaPerStage>();
-      __syncthreads();
-      if (!idle) fold(Stage1{}, c0 + kStageKeys * (ti + 1));
-      __syncthreads();
+    if constexpr (!F8) {
+      issue_stage<LS, W>(stages[0], kpool, vpool, sl, row_bytes, 0, lane, w);
+      for (int ti = 0; ti < ntiles; ti += 2) {
+        issue_stage<LS, W>(stages[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
+        li_wait_vm<kDmaPerStage>();
+        __syncthreads();
+        if (!idle) fold(Stage0{}, c0 + kStageKeys * ti);
+        __syncthreads();
+        if (ti + 1 >= ntiles) break;
+        issue_stage<LS, W>(stages[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
+        li_wait_vm<kDmaPerStage>();
+        __syncthreads();
+        if (!idle) fold(Stage1{}, c0 + kStageKeys * (ti + 1));
+        __syncthreads();
+      }
+    } else {
+      // fp8: the loads fill raw[x]; after the barrier that sees them land,
+      // the work-group converts raw[x] into stages[x], and after a second
+      // barrier the waves fold stages[x]. raw[x] takes its next loads once
+      // converted; stages[x] is converted again only after every wave has
+      // passed the barrier of the stage in between, so after its fold.
+      issue_stage<LS, W>(raw[0], kpool, vpool, sl, row_bytes, 0, lane, w);
+      for (int ti = 0; ti < ntiles; ti += 2) {
+        issue_stage<LS, W>(raw[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
+        li_wait_vm<kDmaPerStage>();
+        __syncthreads();
+        convert_stage<T, W>(lds_addr(raw[0]), lds_addr(stages[0]), tid);
+        __syncthreads();
+        if (!idle) fold(Stage0{}, c0 + kStageKeys * ti);
+        if (ti + 1 >= ntiles) break;
+        issue_stage<LS, W>(raw[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
+        li_wait_vm<kDmaPerStage>();
+        __syncthreads();
+        convert_stage<T, W>(lds_addr(raw[1]), lds_addr(stages[1]), tid);
+        __syncthreads();
+        if (!idle) fold(Stage1{}, c0 + kStageKeys * (ti + 1));
+      }
     }
     li_wait_vm<0>();
   }
@@ -342,7 +398,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   for (int nb = 0; nb < 2; ++nb) {
     const float lt = acc[nb][D / 16][0];
     if (!real[nb]) continue;
-    const float inv = 1.f / lt;
+    const float inv = (F8 ? a.v_scale : 1.f) / lt;
     // acc[nb][blk][r] is dim 16 blk + 4 g + r of this lane's row.
     T* orow = static_cast<T*>(a.out) + (int64_t)tok[nb] * a.o_s0 + (int64_t)head[nb] * a.o_s1 + 4 * g;
 #pragma unroll
@@ -438,9 +494,11 @@ size_t prefill_work_entries(int batch, int max_context) {
 bool prefill_mfma_applies(const AttnArgs& a, int dtype) {
   if (dtype != LI_BF16 && dtype != LI_F16) return false;
   if (a.head_dim != 64 && a.head_dim != 128) return false;
+  if (a.kv_fp8 && a.head_dim != 128) return false;
   if (a.groups < 1 || a.groups > 16) return false;
+  const int pe = a.kv_fp8 ? 1 : 2;
   return rows_aligned(a.q, a.q_s0, a.q_s1, 2) && rows_aligned(a.out, a.o_s0, a.o_s1, 2) &&
-         rows_aligned(a.kp, a.p_s0, a.p_s1, 2) && rows_aligned(a.vp, a.p_s0, a.p_s1, 2);
+         rows_aligned(a.kp, a.p_s0, a.p_s1, pe) && rows_aligned(a.vp, a.p_s0, a.p_s1, pe);
 }
 
 template <int W>
@@ -459,12 +517,16 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
   int64_t grid = (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues;
   grid = std::min<int64_t>(grid, (units + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues);
   const dim3 block(64 * W);
-  if (dtype == LI_BF16) {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W>), dim3((unsigned)grid), block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64, W>), dim3((unsigned)grid), block, 0, s, a);
+  const dim3 g((unsigned)grid);
+  if (a.kv_fp8) {
+    if (dtype == LI_BF16) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true>), g, block, 0, s, a);
+  } else if (dtype == LI_BF16) {
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, false>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64, W, false>), g, block, 0, s, a);
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W>), dim3((unsigned)grid), block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64, W>), dim3((unsigned)grid), block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, false>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64, W, false>), g, block, 0, s, a);
   }
   return check_launch("prefill_mfma");
 }

@@ -322,6 +322,8 @@ def paged_prefill(
     *,
     kernel: str = "auto",
     one_query_rows: bool | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Attend each sequence's chunk of queries over the KV its slots address, causally.
 
@@ -347,6 +349,7 @@ def paged_prefill(
             unknown). The MFMA path hands those to the split decode kernel;
             ``False`` lets the prefill kernel serve every sequence and skips
             the decode launch. Either way the result is the same attention.
+        k_scale, v_scale: the scales of an fp8 pool (see `paged_decode`).
 
     Returns:
         ``[total_queries, num_heads, head_dim]`` with the strides of `query`.
@@ -356,8 +359,7 @@ def paged_prefill(
     device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens, query_start_loc)
     _check_pools(key_pool, value_pool)
     _, num_heads, head_dim = query.shape
-    if query.dtype != key_pool.dtype:
-        raise ValueError(f"query dtype {query.dtype} does not match the pool's {key_pool.dtype}")
+    kv_code = _kv_dtype_code(query, key_pool, k_scale, v_scale)
     if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:
         raise ValueError(
             f"{num_heads} query heads in groups of {num_kv_groups} do not match {key_pool.shape[1]} KV heads"
@@ -385,7 +387,7 @@ def paged_prefill(
     _native.check(status, "paged_prefill")
     out = torch.empty_like(query)
     workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
-    status = lib.li_paged_prefill(
+    status = lib.li_paged_prefill_ex(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
         slot_table.data_ptr(), slot_table.stride(0), max_context,
@@ -393,7 +395,7 @@ def paged_prefill(
         out.data_ptr(), out.stride(0), out.stride(1),
         num_heads, num_kv_heads, head_dim, float(scaling), block_q, block_kv,
         workspace.data_ptr() if workspace is not None else None, need.value,
-        _native.dtype_code(query.dtype),
+        _native.dtype_code(query.dtype), kv_code, float(k_scale), float(v_scale),
         _flags(_prefill_kernel(kernel)) | (_native.LI_FLAG_PREFILL_ONLY if one_query_rows is False else 0),
         _native.stream_handle(device),
     )

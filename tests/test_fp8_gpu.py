@@ -136,3 +136,78 @@ def test_fp8_pool_rejects_what_it_cannot_serve():
     b64 = PagedBatch([40], dtype=torch.bfloat16, num_heads=8, num_kv_heads=2, head_dim=64, num_slots=256)
     with pytest.raises(ValueError, match="MFMA kernel only"):
         paged_decode(b64.query, kp64, kp64.clone(), b64.slot_table, b64.context_lens_t, b64.scaling, b64.groups)
+
+
+def _fp8_packed(context_lens, query_lens, k_scale, v_scale, q_dtype=torch.bfloat16, num_heads=32, num_kv_heads=8,
+                seed=0, num_slots=32768):
+    b = PagedBatch(context_lens, query_lens, dtype=q_dtype, num_heads=num_heads, num_kv_heads=num_kv_heads,
+                   head_dim=128, num_slots=num_slots, seed=seed)
+    kc = fp8.quantize(to_numpy(b.key_pool), k_scale)
+    vc = fp8.quantize(to_numpy(b.value_pool), v_scale)
+    qsl = to_numpy(b.query_start_loc).astype(np.int32)
+    want = attend(to_numpy(b.query), fp8.dequantize(kc, k_scale), fp8.dequantize(vc, v_scale),
+                  b.slot_table.cpu().numpy(), np.asarray(context_lens), b.scaling, b.groups, query_start_loc=qsl,
+                  dtype=np.float64)
+    return b, _to_pool(kc), _to_pool(vc), want
+
+
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("k_scale", "v_scale"), [(1.0, 1.0), (0.05, 0.2)])
+@pytest.mark.parametrize("one_query_rows", [None, False])
+def test_fp8_prefill_matches_the_oracle_over_dequantised_rows(q_dtype, k_scale, v_scale, one_query_rows):
+    """Chunks over prefixes and alone, straddling stage boundaries, beside one-query rows."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    ctx = [1, 40, 300, 129, 64, 700, 1500]
+    q = [1, 33, 200, 1, 64, 31, 257]
+    b, kp, vp, want = _fp8_packed(ctx, q, k_scale, v_scale, q_dtype=q_dtype, seed=7)
+    out = paged_prefill(b.query, kp, vp, b.slot_table, b.context_lens_t, b.query_start_loc, max(q), b.scaling,
+                        b.groups, one_query_rows=one_query_rows, k_scale=k_scale, v_scale=v_scale)
+    assert_within(out, want, 2e-2, 2e-3)
+
+
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(8, 8), (16, 1), (32, 16)])
+def test_fp8_prefill_groupings(num_heads, num_kv_heads):
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    ctx, q = [90, 5000, 33], [90, 130, 1]
+    b, kp, vp, want = _fp8_packed(ctx, q, 0.5, 2.0, num_heads=num_heads, num_kv_heads=num_kv_heads, seed=8)
+    out = paged_prefill(b.query, kp, vp, b.slot_table, b.context_lens_t, b.query_start_loc, max(q), b.scaling,
+                        b.groups, k_scale=0.5, v_scale=2.0)
+    assert_within(out, want, 2e-2, 2e-3)
+
+
+def test_cache_layer_fp8_pool_end_to_end():
+    """BlockPool(cache_quant="fp8") through KVCache payloads and the `paged` boundary: the
+    same answer as the dense eager kernel reading the same fp8 pool (which dequantises)."""
+    from liteinfer_amd.attention import eager_attention, paged_attention
+    from liteinfer_amd.cache.block_pool import BlockPool
+    from liteinfer_amd.cache.kv_cache import KVCache
+
+    g = torch.Generator(device=DEV).manual_seed(9)
+    pool = BlockPool(256, 16, 2, 8, 128, torch.bfloat16, DEV, cache_quant="fp8", k_scale=0.5, v_scale=0.25)
+    cache = KVCache(pool)
+    ids, prompts = ["a", "b", "c"], [37, 300, 129]
+    cache.reserve(ids, prompts)
+    payload = cache.make_packed_payload(ids, [0, 0, 0], prompts)
+    t = sum(prompts)
+    q = torch.randn(1, 32, t, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(1, 8, t, 128, generator=g, device=DEV).to(torch.bfloat16)
+    v = torch.randn(1, 8, t, 128, generator=g, device=DEV).to(torch.bfloat16)
+    kv = payload.update(k, v, 1)
+    assert kv.key_pool.dtype == FP8 and kv.k_scale == 0.5 and kv.v_scale == 0.25
+    out = paged_attention(q, kv, 128 ** -0.5, 4)
+    ref = eager_attention(q.float(), kv._replace(), 128 ** -0.5, 4)
+    assert_within(out, to_numpy(ref).astype(np.float64), 2e-2, 2e-3)
+    # A decode step over the same contexts, one new token each.
+    totals = [p + 1 for p in prompts]
+    cache.reserve(ids, totals)
+    dec = cache.make_decode_payload(cache.newest_slots_for(ids, prompts), cache.slot_table_for(ids, totals),
+                                    torch.tensor(totals, dtype=torch.int32, device=DEV))
+    qd = torch.randn(3, 32, 1, 128, generator=g, device=DEV).to(torch.bfloat16)
+    kd = torch.randn(3, 8, 1, 128, generator=g, device=DEV).to(torch.bfloat16)
+    vd = torch.randn(3, 8, 1, 128, generator=g, device=DEV).to(torch.bfloat16)
+    kvd = dec.update(kd, vd, 1)
+    outd = paged_attention(qd, kvd, 128 ** -0.5, 4)
+    refd = eager_attention(qd.float(), kvd, 128 ** -0.5, 4)
+    assert_within(outd, to_numpy(refd).astype(np.float64), 2e-2, 2e-3)
