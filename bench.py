@@ -14,7 +14,8 @@ decode call (the partition kernel plus the partition combine, timed with HIP
 events on the stream they run on) against MI355X's 8 TB/s. Config 3's packed
 prefill (TFLOP/s of visible causal pairs; also its 8 chunks alone, its 56
 one-query rows alone in GB/s, and 8 chunks of 2048 queries over 8192 cached
-keys) and config 4's long-context decode are reported beside it, and so is the fused RoPE + slot-write at config 3's
+keys) and config 4's long-context decode are reported beside it, each also
+over an fp8 (e4m3) KV pool, and so is the fused RoPE + slot-write at config 3's
 packed pass and config 2's decode step, with the reference's separate torch
 ops timed on the same inputs, and config 5: `LLM.generate` of 256 requests x
 256 greedy tokens over a random-initialised Llama-3-8B-architecture model
@@ -44,6 +45,7 @@ sys.path.insert(0, str(ROOT))
 from liteinfer_amd import _native  # noqa: E402
 from liteinfer_amd.attention import PagedKV, paged_attention  # noqa: E402
 from liteinfer_amd.cache.kv_cache import scatter_into  # noqa: E402
+from liteinfer_amd.paged_kernels import kv_scatter  # noqa: E402
 from liteinfer_amd.workloads import c3_shapes, decode_step, packed_step  # noqa: E402
 
 METRIC = "paged-decode HBM GB/s (% of peak); prefill attn TFLOP/s; e2e output tok/s"
@@ -52,10 +54,24 @@ BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "decode_c2_traffic.json"
 
 
-def decode_bytes(ctxs, geo, elem=2) -> int:
-    """K and V rows of every context token for all KV heads, its int64 slot, q in and out."""
+def decode_bytes(ctxs, geo, elem=2, kv_elem=None) -> int:
+    """K and V rows of every context token for all KV heads, its int64 slot, q in and out.
+
+    kv_elem: bytes per pool element when the pool's type differs from q's (1 for an fp8 pool).
+    """
     tokens = sum(ctxs)
-    return tokens * (2 * geo.num_kv_heads * geo.head_dim * elem + 8) + 2 * len(ctxs) * geo.num_heads * geo.head_dim * elem
+    kv = elem if kv_elem is None else kv_elem
+    return tokens * (2 * geo.num_kv_heads * geo.head_dim * kv + 8) + 2 * len(ctxs) * geo.num_heads * geo.head_dim * elem
+
+
+def to_fp8_pool(step):
+    """The step with its pools quantised to fp8 (e4m3, scales 1) by the slot-write kernel."""
+    kp = torch.empty(step.key_pool.shape, dtype=torch.float8_e4m3fn, device=step.key_pool.device)
+    vp = torch.empty_like(kp)
+    every = torch.arange(kp.shape[0], device=kp.device).view(1, -1)
+    kv_scatter(kp, vp, every, step.key_pool.unsqueeze(0).transpose(1, 2), step.value_pool.unsqueeze(0).transpose(1, 2))
+    step.key_pool, step.value_pool = kp, vp
+    return step
 
 
 def scatter_bytes(tokens, geo, elem=2) -> int:
@@ -317,7 +333,30 @@ def main() -> int:
             "frac_hbm": round(c4_bytes / (c4_avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "context_tokens": sum(c4.host_context_lens),
         }
+        # The same decode steps over an fp8 (e4m3) pool: half the K/V bytes.
+        c4 = to_fp8_pool(c4)
+        _, c4_ms8 = _time_decode(c4, max(10, args.steps // 4), 3)
+        c4_bytes8 = decode_bytes(c4.host_context_lens, c4.geometry, kv_elem=1)
+        c4_avg8 = statistics.mean(c4_ms8)
+        secondary["decode_c4_fp8_kv"] = {
+            "avg_us": round(c4_avg8 * 1e3, 2),
+            "GB/s": round(c4_bytes8 / (c4_avg8 * 1e-3) / 1e9, 1),
+            "frac_hbm": round(c4_bytes8 / (c4_avg8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "speedup_vs_bf16_kv": round(c4_avg / c4_avg8, 3),
+        }
         del c4
+        torch.cuda.empty_cache()
+        c2 = to_fp8_pool(decode_step("c2", seed=args.seed))
+        _, c2_ms8 = _time_decode(c2, max(10, args.steps // 4), 3)
+        c2_bytes8 = decode_bytes(c2.host_context_lens, c2.geometry, kv_elem=1)
+        c2_avg8 = statistics.mean(c2_ms8)
+        secondary["decode_c2_fp8_kv"] = {
+            "avg_us": round(c2_avg8 * 1e3, 2),
+            "GB/s": round(c2_bytes8 / (c2_avg8 * 1e-3) / 1e9, 1),
+            "frac_hbm": round(c2_bytes8 / (c2_avg8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "speedup_vs_bf16_kv": round(decode_avg_ms / c2_avg8, 3),
+        }
+        del c2
         torch.cuda.empty_cache()
         c3 = packed_step("c3", seed=args.seed)
         c3_ms = _time_prefill(c3, max(10, args.steps // 4), 3)
@@ -331,6 +370,13 @@ def main() -> int:
             "query_tokens": sum(c3.host_query_lens),
         }
         geo3, c3_tokens = c3.geometry, sum(c3.host_query_lens)
+        c3 = to_fp8_pool(c3)
+        c3_avg8 = statistics.mean(_time_prefill(c3, max(10, args.steps // 4), 3))
+        secondary["prefill_c3_fp8_kv"] = {
+            "avg_us": round(c3_avg8 * 1e3, 2),
+            "TFLOP/s": round(flops / (c3_avg8 * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(flops / (c3_avg8 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        }
         del c3
         torch.cuda.empty_cache()
         # Config 3's two kinds of work on their own: the 8 chunks (MFMA-bound)
@@ -377,6 +423,8 @@ def main() -> int:
         from liteinfer_amd.engine import e2e
 
         result.setdefault("secondary", {})["e2e_c5"] = e2e.run(seed=args.seed)
+        torch.cuda.empty_cache()
+        result["secondary"]["e2e_c5_fp8_kv"] = e2e.run(seed=args.seed, cache_quant="fp8")
         torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:

@@ -136,6 +136,26 @@ int li_rope_kv_write(const void* q, const int64_t* q_strides, const void* k,
                      void* stream);
 
 /*
+ * li_rope_kv_write into fp8 (LI_FP8_E4M3) pools: q_out as li_rope_kv_write
+ * makes it; the rotated k (rounded to `dtype` exactly as li_rope_kv_write
+ * rounds it) and v stored as li_kv_scatter_fp8 stores them, so the pool
+ * bytes equal RoPE followed by li_kv_scatter_fp8. dtype is LI_BF16 or LI_F16;
+ * rows 16-byte aligned with a contiguous last axis (otherwise
+ * LI_EUNSUPPORTED). No counterpart in the reference's code (its planned
+ * quantised cache, docs/roadmap.md 2.5).
+ */
+int li_rope_kv_write_fp8(const void* q, const int64_t* q_strides, const void* k,
+                         const int64_t* k_strides, const void* v,
+                         const int64_t* v_strides, const void* cos, const void* sin,
+                         const int64_t* cs_strides, int64_t batch, int64_t tokens,
+                         const int64_t* slots, void* q_out,
+                         const int64_t* q_out_strides, void* key_pool,
+                         void* value_pool, int64_t num_slots,
+                         int64_t pool_stride_slot, int64_t pool_stride_head,
+                         int num_heads, int num_kv_heads, int head_dim, int dtype,
+                         float k_scale, float v_scale, void* stream);
+
+/*
  * How many partitions each sequence's key loop is cut into for a decode step
  * of `batch` rows over a slot table `max_context` wide, on a device of
  * `num_cus` compute units (0 = ask the current device). Counterpart of

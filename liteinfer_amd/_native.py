@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "li_kv_scatter",
     "li_kv_scatter_fp8",
     "li_rope_kv_write",
+    "li_rope_kv_write_fp8",
     "li_choose_num_splits",
     "li_paged_decode_plan",
     "li_paged_decode",
@@ -62,6 +63,11 @@ _SIGNATURES = {
         _i32,
         [_p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64p, _i64, _i64, _p, _p, _i64p, _p, _p,
          _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p],
+    ),
+    "li_rope_kv_write_fp8": (
+        _i32,
+        [_p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64p, _i64, _i64, _p, _p, _i64p, _p, _p,
+         _i64, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _f32, _p],
     ),
     "li_choose_num_splits": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "li_paged_decode_plan": (

@@ -149,10 +149,11 @@ class KVCache:
         of llama.py:85-98 and `scatter` on the CPU.
         """
         keys, values = self._pool.slots(layer_idx)
-        if keys.device.type == "cuda" and self._pool.cache_quant is None:
+        if keys.device.type == "cuda":
             from liteinfer_amd.rope import rope_kv_write
 
-            return rope_kv_write(q, k, v, cos, sin, slots, keys, values)
+            return rope_kv_write(q, k, v, cos, sin, slots, keys, values,
+                                 k_scale=self._pool.k_scale, v_scale=self._pool.v_scale)
         from liteinfer_amd.rope import apply_rotary_pos_emb
 
         q_embed, k_embed = apply_rotary_pos_emb(q, k, cos, sin)

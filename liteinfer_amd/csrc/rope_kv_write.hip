@@ -27,6 +27,8 @@
 // the slot list, _tokens_first, kv_cache.py:250-253).
 #include "li_common.h"
 
+#include <cmath>
+
 namespace {
 
 struct RopeArgs {
@@ -46,7 +48,23 @@ struct RopeArgs {
   int64_t num_slots;
   int64_t ps_slot, ps_head;
   int num_heads, num_kv_heads, head_dim;
+  float inv_k, inv_v;  // fp8 pools: 1 / k_scale, 1 / v_scale
 };
+
+// Eight values, rounded to E (as stored by the unfused path), to eight e4m3
+// bytes: e4m3(clamp(float(x) * inv, +-448)), as li_kv_scatter_fp8 stores them.
+template <typename VecE>
+__device__ __forceinline__ uint2 quant8(VecE x, float inv) {
+  float f[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(li_to_float(x[e]) * inv, -448.f), 448.f);
+  uint2 out;
+  out.x = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0u, false);
+  out.x = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], out.x, true);
+  out.y = __builtin_amdgcn_cvt_pk_fp8_f32(f[4], f[5], 0u, false);
+  out.y = __builtin_amdgcn_cvt_pk_fp8_f32(f[6], f[7], out.y, true);
+  return out;
+}
 
 template <typename E>
 struct Lanes;
@@ -87,7 +105,9 @@ __device__ __forceinline__ void rotate(E lo, E hi, E c_lo, E s_lo, E c_hi, E s_h
 // sizeof(E)), unit dim strides.
 // I: the index type of the work-item arithmetic (32-bit whenever the total
 // fits, which spares the 64-bit division sequences).
-template <typename E, typename I>
+// F8: the pools are fp8 (e4m3): the rotated k (rounded to E, as the torch ops
+// round it) and v are quantised on the way in, 8 bytes per half chunk.
+template <typename E, typename I, bool F8>
 __global__ __launch_bounds__(256) void rope_kv_write_vec(RopeArgs a) {
   constexpr int kE = Lanes<E>::kPer16;
   typedef E vecE __attribute__((ext_vector_type(kE)));
@@ -108,24 +128,32 @@ __global__ __launch_bounds__(256) void rope_kv_write_vec(RopeArgs a) {
       const int64_t slot = a.slots[i];
       if (slot < 0 || slot >= a.num_slots) continue;
       const E* src = reinterpret_cast<const E*>(a.v) + b * a.vs[0] + h * a.vs[1] + t * a.vs[2] + d0;
-      E* dst = reinterpret_cast<E*>(a.vp) + slot * a.ps_slot + h * a.ps_head + d0;
-      const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(src);
-      const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(src + half);
-      *reinterpret_cast<u32x4_t*>(dst) = lo;
-      *reinterpret_cast<u32x4_t*>(dst + half) = hi;
+      if constexpr (F8) {
+        uint8_t* dst = reinterpret_cast<uint8_t*>(a.vp) + slot * a.ps_slot + h * a.ps_head + d0;
+        *reinterpret_cast<uint2*>(dst) = quant8(*reinterpret_cast<const vecE*>(src), a.inv_v);
+        *reinterpret_cast<uint2*>(dst + half) = quant8(*reinterpret_cast<const vecE*>(src + half), a.inv_v);
+      } else {
+        E* dst = reinterpret_cast<E*>(a.vp) + slot * a.ps_slot + h * a.ps_head + d0;
+        const u32x4_t lo = *reinterpret_cast<const u32x4_t*>(src);
+        const u32x4_t hi = *reinterpret_cast<const u32x4_t*>(src + half);
+        *reinterpret_cast<u32x4_t*>(dst) = lo;
+        *reinterpret_cast<u32x4_t*>(dst + half) = hi;
+      }
       continue;
     }
     const bool is_q = hh < a.num_heads;
     const int h = is_q ? hh : hh - a.num_heads;
     const E* src = is_q ? reinterpret_cast<const E*>(a.q) + b * a.qs[0] + h * a.qs[1] + t * a.qs[2] + d0
                         : reinterpret_cast<const E*>(a.k) + b * a.ks[0] + h * a.ks[1] + t * a.ks[2] + d0;
-    E* dst;
+    E* dst = nullptr;
+    uint8_t* dst8 = nullptr;
     if (is_q) {
       dst = reinterpret_cast<E*>(a.qo) + b * a.os[0] + h * a.os[1] + t * a.os[2] + d0;
     } else {
       const int64_t slot = a.slots[i];
       if (slot < 0 || slot >= a.num_slots) continue;
-      dst = reinterpret_cast<E*>(a.kp) + slot * a.ps_slot + h * a.ps_head + d0;
+      if constexpr (F8) dst8 = reinterpret_cast<uint8_t*>(a.kp) + slot * a.ps_slot + h * a.ps_head + d0;
+      else dst = reinterpret_cast<E*>(a.kp) + slot * a.ps_slot + h * a.ps_head + d0;
     }
     const int64_t co = b * a.cs[0] + t * a.cs[1] + d0;
     const vecE xl = *reinterpret_cast<const vecE*>(src);
@@ -142,8 +170,13 @@ __global__ __launch_bounds__(256) void rope_kv_write_vec(RopeArgs a) {
       ol[e] = lo;
       oh[e] = hi;
     }
-    *reinterpret_cast<vecE*>(dst) = ol;
-    *reinterpret_cast<vecE*>(dst + half) = oh;
+    if (F8 && !is_q) {
+      *reinterpret_cast<uint2*>(dst8) = quant8(ol, a.inv_k);
+      *reinterpret_cast<uint2*>(dst8 + half) = quant8(oh, a.inv_k);
+    } else {
+      *reinterpret_cast<vecE*>(dst) = ol;
+      *reinterpret_cast<vecE*>(dst + half) = oh;
+    }
   }
 }
 
@@ -201,7 +234,9 @@ __global__ __launch_bounds__(256) void rope_kv_write_elem(RopeArgs a) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-bool vec_ok(const RopeArgs& a, int esize) {
+// pool_esize: bytes per pool element (1 for an fp8 pool, whose half-rows of
+// 8 elements take 8-byte stores).
+bool vec_ok(const RopeArgs& a, int esize, int pool_esize) {
   const int per16 = 16 / esize;
   if (a.head_dim % (2 * per16) != 0) return false;
   if (a.qs[3] != 1 || a.ks[3] != 1 || a.vs[3] != 1 || a.os[3] != 1 || a.cs[2] != 1) return false;
@@ -209,25 +244,33 @@ bool vec_ok(const RopeArgs& a, int esize) {
   for (const char* p : ptrs)
     if (!aligned16(p)) return false;
   const int64_t strides[] = {a.qs[0], a.qs[1], a.qs[2], a.ks[0], a.ks[1], a.ks[2], a.vs[0], a.vs[1], a.vs[2],
-                             a.os[0], a.os[1], a.os[2], a.cs[0], a.cs[1], a.ps_slot, a.ps_head};
+                             a.os[0], a.os[1], a.os[2], a.cs[0], a.cs[1]};
   for (int64_t s : strides)
     if ((s * esize) % 16 != 0) return false;
-  return true;
+  const int pool_align = pool_esize == esize ? 16 : 8;
+  return (a.ps_slot * pool_esize) % pool_align == 0 && (a.ps_head * pool_esize) % pool_align == 0 &&
+         (a.head_dim / 2 * pool_esize) % pool_align == 0;
 }
 
 }  // namespace
 
-extern "C" int li_rope_kv_write(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
-                                const void* v, const int64_t* v_strides, const void* cos, const void* sin,
-                                const int64_t* cs_strides, int64_t batch, int64_t tokens, const int64_t* slots,
-                                void* q_out, const int64_t* q_out_strides, void* key_pool, void* value_pool,
-                                int64_t num_slots, int64_t pool_stride_slot, int64_t pool_stride_head, int num_heads,
-                                int num_kv_heads, int head_dim, int dtype, void* stream) {
+namespace {
+
+int rope_impl(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides, const void* v,
+              const int64_t* v_strides, const void* cos, const void* sin, const int64_t* cs_strides, int64_t batch,
+              int64_t tokens, const int64_t* slots, void* q_out, const int64_t* q_out_strides, void* key_pool,
+              void* value_pool, int64_t num_slots, int64_t pool_stride_slot, int64_t pool_stride_head, int num_heads,
+              int num_kv_heads, int head_dim, int dtype, bool fp8, float k_scale, float v_scale, void* stream) {
   li::clear_error();
   const int esize = li::dtype_size(dtype);
   if (esize == 0) return li::fail(LI_EINVAL, "li_rope_kv_write: unknown dtype %d", dtype);
   if (dtype == LI_FP8_E4M3)
-    return li::fail(LI_EUNSUPPORTED, "li_rope_kv_write: fp8 pools are written by li_kv_scatter_fp8 (quantising), not copied");
+    return li::fail(LI_EUNSUPPORTED, "li_rope_kv_write: fp8 pools are written by li_rope_kv_write_fp8 (quantising)");
+  if (fp8 && dtype == LI_F32)
+    return li::fail(LI_EUNSUPPORTED, "li_rope_kv_write_fp8: bf16 / fp16 projections only");
+  if (fp8 && (!(k_scale > 0.f) || !(v_scale > 0.f) || !std::isfinite(k_scale) || !std::isfinite(v_scale)))
+    return li::fail(LI_EINVAL, "li_rope_kv_write_fp8: scales must be finite and > 0 (k_scale=%g, v_scale=%g)",
+                    k_scale, v_scale);
   if (batch < 0 || tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || num_slots < 0)
     return li::fail(LI_EINVAL, "li_rope_kv_write: negative or empty extent");
   if (head_dim % 2 != 0) return li::fail(LI_EINVAL, "li_rope_kv_write: head_dim %d is odd", head_dim);
@@ -266,22 +309,40 @@ extern "C" int li_rope_kv_write(const void* q, const int64_t* q_strides, const v
   a.num_heads = num_heads;
   a.num_kv_heads = num_kv_heads;
   a.head_dim = head_dim;
+  a.inv_k = fp8 ? 1.f / k_scale : 1.f;
+  a.inv_v = fp8 ? 1.f / v_scale : 1.f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int threads = 256;
   const int heads = num_heads + 2 * num_kv_heads;
-  if (vec_ok(a, esize)) {
+  if (fp8) {
+    // fp8 pool rows take 8-byte stores: byte strides multiples of 8.
+    if (!vec_ok(a, esize, /*pool_esize=*/1))
+      return li::fail(LI_EUNSUPPORTED, "li_rope_kv_write_fp8: rows must be 16-byte aligned with a contiguous last axis");
+    const int64_t work = n * heads * (head_dim / 2 / 8);
+    const int64_t blocks = std::min<int64_t>(li::cdiv64(work, threads), 65536);
+    const dim3 grid((unsigned)blocks), block(threads);
+    if (work < (int64_t)1 << 31) {
+      if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, uint32_t, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, uint32_t, true>), grid, block, 0, s, a);
+    } else {
+      if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, int64_t, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, int64_t, true>), grid, block, 0, s, a);
+    }
+    return li::check_launch("li_rope_kv_write_fp8");
+  }
+  if (vec_ok(a, esize, esize)) {
     const int64_t work = n * heads * (head_dim / 2 / (16 / esize));
     const int64_t blocks = std::min<int64_t>(li::cdiv64(work, threads), 65536);
     const dim3 grid((unsigned)blocks), block(threads);
     if (work < (int64_t)1 << 31) {
-      if (dtype == LI_F32) hipLaunchKernelGGL((rope_kv_write_vec<float, uint32_t>), grid, block, 0, s, a);
-      else if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, uint32_t>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, uint32_t>), grid, block, 0, s, a);
+      if (dtype == LI_F32) hipLaunchKernelGGL((rope_kv_write_vec<float, uint32_t, false>), grid, block, 0, s, a);
+      else if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, uint32_t, false>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, uint32_t, false>), grid, block, 0, s, a);
     } else {
-      if (dtype == LI_F32) hipLaunchKernelGGL((rope_kv_write_vec<float, int64_t>), grid, block, 0, s, a);
-      else if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, int64_t>), grid, block, 0, s, a);
-      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, int64_t>), grid, block, 0, s, a);
+      if (dtype == LI_F32) hipLaunchKernelGGL((rope_kv_write_vec<float, int64_t, false>), grid, block, 0, s, a);
+      else if (dtype == LI_BF16) hipLaunchKernelGGL((rope_kv_write_vec<li_bf16, int64_t, false>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((rope_kv_write_vec<li_f16, int64_t, false>), grid, block, 0, s, a);
     }
   } else {
     const int64_t work = n * heads * (head_dim / 2);
@@ -291,4 +352,29 @@ extern "C" int li_rope_kv_write(const void* q, const int64_t* q_strides, const v
     else hipLaunchKernelGGL(rope_kv_write_elem<li_f16>, dim3((unsigned)blocks), dim3(threads), 0, s, a);
   }
   return li::check_launch("li_rope_kv_write");
+}
+
+}  // namespace
+
+extern "C" int li_rope_kv_write(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                                const void* v, const int64_t* v_strides, const void* cos, const void* sin,
+                                const int64_t* cs_strides, int64_t batch, int64_t tokens, const int64_t* slots,
+                                void* q_out, const int64_t* q_out_strides, void* key_pool, void* value_pool,
+                                int64_t num_slots, int64_t pool_stride_slot, int64_t pool_stride_head, int num_heads,
+                                int num_kv_heads, int head_dim, int dtype, void* stream) {
+  return rope_impl(q, q_strides, k, k_strides, v, v_strides, cos, sin, cs_strides, batch, tokens, slots, q_out,
+                   q_out_strides, key_pool, value_pool, num_slots, pool_stride_slot, pool_stride_head, num_heads,
+                   num_kv_heads, head_dim, dtype, false, 1.f, 1.f, stream);
+}
+
+extern "C" int li_rope_kv_write_fp8(const void* q, const int64_t* q_strides, const void* k,
+                                    const int64_t* k_strides, const void* v, const int64_t* v_strides,
+                                    const void* cos, const void* sin, const int64_t* cs_strides, int64_t batch,
+                                    int64_t tokens, const int64_t* slots, void* q_out, const int64_t* q_out_strides,
+                                    void* key_pool, void* value_pool, int64_t num_slots, int64_t pool_stride_slot,
+                                    int64_t pool_stride_head, int num_heads, int num_kv_heads, int head_dim, int dtype,
+                                    float k_scale, float v_scale, void* stream) {
+  return rope_impl(q, q_strides, k, k_strides, v, v_strides, cos, sin, cs_strides, batch, tokens, slots, q_out,
+                   q_out_strides, key_pool, value_pool, num_slots, pool_stride_slot, pool_stride_head, num_heads,
+                   num_kv_heads, head_dim, dtype, true, k_scale, v_scale, stream);
 }

@@ -32,9 +32,9 @@ def prompts(seed: int = 0, n: int = NUM_REQUESTS, vocab: int = LLAMA_3_8B.vocab_
 
 
 def run(seed: int = 0, config: EngineConfig | None = None, num_requests: int = NUM_REQUESTS,
-        output_tokens: int = OUTPUT_TOKENS) -> dict:
+        output_tokens: int = OUTPUT_TOKENS, cache_quant: str | None = None) -> dict:
     config = config or EngineConfig(max_num_seqs=256, max_model_len=PROMPT_CLIP[1] + OUTPUT_TOKENS,
-                                    max_num_batched_tokens=8192, num_gpu_blocks=32768)
+                                    max_num_batched_tokens=8192, num_gpu_blocks=32768, cache_quant=cache_quant)
     model = RandomLlama(LLAMA_3_8B, seed=seed)
     llm = LLM(model, config)
     # warm-up: kernels, allocator, and every decode graph width
@@ -56,6 +56,7 @@ def run(seed: int = 0, config: EngineConfig | None = None, num_requests: int = N
         "max_num_seqs": config.max_num_seqs,
         "max_num_batched_tokens": config.max_num_batched_tokens,
         "decode_graphs": config.use_graphs,
+        "kv_cache": config.cache_quant or "bf16",
         "parameter_bytes": model.parameter_bytes(),
     }
 

@@ -27,6 +27,10 @@ class EngineConfig:
     num_gpu_blocks: int = 24576
     block_size: int = 16
     use_graphs: bool = True
+    cache_quant: str | None = None
+    """None (the model dtype) or "fp8": K/V stored as e4m3 with `k_scale` / `v_scale`."""
+    k_scale: float = 1.0
+    v_scale: float = 1.0
 
 
 @dataclass
@@ -48,7 +52,8 @@ class LLM:
         self.config = config
         self.model = model
         pool = BlockPool(num_blocks=config.num_gpu_blocks, block_size=config.block_size, num_layers=s.num_layers,
-                         num_kv_heads=s.num_kv_heads, head_dim=s.head_dim, dtype=model.dtype, device=model.device)
+                         num_kv_heads=s.num_kv_heads, head_dim=s.head_dim, dtype=model.dtype, device=model.device,
+                         cache_quant=config.cache_quant, k_scale=config.k_scale, v_scale=config.v_scale)
         self.cache = KVCache(pool)
         self.runner = ModelRunner(model, self.cache, config.max_num_seqs, config.max_model_len, config.use_graphs)
         self.scheduler = Scheduler(config.max_num_seqs, config.max_num_batched_tokens)

@@ -41,6 +41,9 @@ def rope_kv_write(
     slots: torch.Tensor,
     key_pool: torch.Tensor,
     value_pool: torch.Tensor,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Rotate q and k, store k and v at `slots`, return the rotated q.
 
@@ -53,7 +56,10 @@ def rope_kv_write(
         slots: ``batch * tokens`` pool slots, batch-major (``[1, T]`` for a
             packed pass, ``[1, B]`` for a decode step).
         key_pool, value_pool: this layer's ``[num_slots, num_kv_heads,
-            head_dim]`` stores, written in place.
+            head_dim]`` stores, written in place. An fp8
+            (``torch.float8_e4m3fn``) pool stores the rotated k (rounded to
+            q's dtype, as the torch ops round it) and v quantised with
+            `k_scale` / `v_scale`, exactly as `kv_scatter` would store them.
 
     Returns:
         The rotated q, ``[batch, num_heads, tokens, head_dim]``, laid out
@@ -73,7 +79,10 @@ def rope_kv_write(
         raise ValueError(f"k rows {num_kv_heads}x{head_dim} do not match the pool's {tuple(key_pool.shape[1:])}")
     if head_dim % 2:
         raise ValueError(f"head_dim {head_dim} must be even for rotary embedding")
-    dtype = key_pool.dtype
+    fp8 = key_pool.dtype == _native.FP8_POOL_DTYPE
+    dtype = q.dtype if fp8 else key_pool.dtype
+    if fp8 and dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"an fp8 pool is written from bfloat16 or float16 projections, not {dtype}")
     for name, t in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
         if t.dtype != dtype:
             raise ValueError(f"{name} dtype {t.dtype} does not match the pool's {dtype}")
@@ -90,7 +99,7 @@ def rope_kv_write(
         raise ValueError(f"{flat_slots.numel()} slots for {batch * tokens} tokens")
     out = torch.empty(batch, tokens, num_heads, head_dim, dtype=dtype, device=device).transpose(1, 2)
     lib = _native.load()
-    status = lib.li_rope_kv_write(
+    args = (
         q.data_ptr(), _native.i64_array(q.stride()),
         k.data_ptr(), _native.i64_array(k.stride()),
         v.data_ptr(), _native.i64_array(v.stride()),
@@ -100,7 +109,12 @@ def rope_kv_write(
         key_pool.data_ptr(), value_pool.data_ptr(),
         key_pool.shape[0], key_pool.stride(0), key_pool.stride(1),
         num_heads, num_kv_heads, head_dim, _native.dtype_code(dtype),
-        _native.stream_handle(device),
     )
+    if fp8:
+        if not (k_scale > 0 and v_scale > 0):
+            raise ValueError(f"k_scale and v_scale must be > 0, got {k_scale}, {v_scale}")
+        status = lib.li_rope_kv_write_fp8(*args, float(k_scale), float(v_scale), _native.stream_handle(device))
+    else:
+        status = lib.li_rope_kv_write(*args, _native.stream_handle(device))
     _native.check(status, "rope_kv_write")
     return out

@@ -96,3 +96,24 @@ def test_bf16_engine_logits_track_the_dense_forward():
     for prompt, out in zip(prompts, outputs):
         want = _dense_logits(model, prompt).float()
         assert int(want.argmax()) == out[0] or want.topk(2).values.diff().abs().item() < 0.05
+
+
+TINY128 = LlamaShape(hidden_size=512, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=128,
+                     intermediate_size=1024, vocab_size=1000)
+
+
+@pytest.mark.parametrize("use_graphs", [True, False])
+def test_fp8_cache_engine_logits_track_the_dense_forward(use_graphs):
+    """The engine over an fp8 (e4m3) KV cache: its first tokens follow the dense bf16 forward,
+    up to near-ties the cache's rounding may flip."""
+    model = RandomLlama(TINY128, dtype=torch.bfloat16, seed=4, std=0.05)
+    config = EngineConfig(max_num_seqs=8, max_model_len=512, max_num_batched_tokens=256, num_gpu_blocks=256,
+                          use_graphs=use_graphs, cache_quant="fp8", k_scale=0.5, v_scale=0.5)
+    llm = LLM(model, config)
+    assert llm.cache.pool.cache_quant == "fp8"
+    prompts = _prompts(5, 40, 200, TINY128.vocab_size, seed=5)
+    outputs, stats = llm.generate(prompts, max_tokens=3)
+    assert stats.output_tokens == 15
+    for prompt, out in zip(prompts, outputs):
+        want = _dense_logits(model, prompt).float()
+        assert int(want.argmax()) == out[0] or want.topk(2).values.diff().abs().item() < 0.1

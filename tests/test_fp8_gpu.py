@@ -211,3 +211,31 @@ def test_cache_layer_fp8_pool_end_to_end():
     outd = paged_attention(qd, kvd, 128 ** -0.5, 4)
     refd = eager_attention(qd.float(), kvd, 128 ** -0.5, 4)
     assert_within(outd, to_numpy(refd).astype(np.float64), 2e-2, 2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize(("batch", "tokens"), [(1, 37), (5, 1)])
+def test_fused_rope_write_into_fp8_pools_is_rope_then_quantising_scatter(dtype, batch, tokens):
+    """li_rope_kv_write_fp8 stores exactly what the torch rotation followed by the quantising
+    slot-write stores, and returns the same rotated q as the bf16 / fp16 fused kernel."""
+    from liteinfer_amd.rope import apply_rotary_pos_emb, rope_kv_write
+
+    g = torch.Generator(device=DEV).manual_seed(10)
+    heads, kvh, d, num_slots = 32, 8, 128, 512
+    q = torch.randn(batch, tokens, heads, d, generator=g, device=DEV).to(dtype).transpose(1, 2)
+    k = (torch.randn(batch, tokens, kvh, d, generator=g, device=DEV) * 20).to(dtype).transpose(1, 2)
+    v = (torch.randn(batch, tokens, kvh, d, generator=g, device=DEV) * 20).to(dtype).transpose(1, 2)
+    ang = torch.rand(batch, tokens, d, generator=g, device=DEV) * 6.28
+    cos, sin = ang.cos().to(dtype), ang.sin().to(dtype)
+    slots = torch.randperm(num_slots, device=DEV)[: batch * tokens].view(1, -1)
+    kp = torch.zeros(num_slots, kvh, d, dtype=FP8, device=DEV)
+    vp = torch.zeros_like(kp)
+    q_out = rope_kv_write(q, k, v, cos, sin, slots, kp, vp, k_scale=0.5, v_scale=4.0)
+    want_q, k_rot = apply_rotary_pos_emb(q, k, cos, sin)
+    kp2, vp2 = torch.zeros_like(kp), torch.zeros_like(vp)
+    kv_scatter(kp2, vp2, slots, k_rot, v, k_scale=0.5, v_scale=4.0)
+    assert torch.equal(kp.view(torch.uint8), kp2.view(torch.uint8))
+    assert torch.equal(vp.view(torch.uint8), vp2.view(torch.uint8))
+    kp3 = torch.zeros(num_slots, kvh, d, dtype=dtype, device=DEV)
+    q16 = rope_kv_write(q, k, v, cos, sin, slots, kp3, torch.zeros_like(kp3))
+    assert torch.equal(q_out, q16) and torch.equal(q_out, want_q)
