@@ -307,7 +307,7 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "roofline": {
-            "kernel": "paged decode call (decode_balanced + combine_balanced)",
+            "kernel": "paged decode call (decode_grouped + combine_balanced)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,

@@ -91,35 +91,107 @@ struct DecodeState {
   floatx4_t acc[8];
 };
 
-// Folds keys [kb, ke) of sequence `seq`'s context for KV head `kvh` into `st`.
-// qf holds this lane's head's query (zeros for heads past the group).
+// Per-lane LDS byte offsets within a tile: the K operand of key n, step j
+// (key 16 + n sits L::kRow16 bytes below), and the V^T reads' addresses
+// (li_read_vt's two for 16-bit rows, the one 8-bit transposing read for
+// fp8 rows; see F8Tile).
+template <int D, bool F8>
+struct TileOffsets {
+  uint32_t koff[D / 32], voff[D / 16];
+  __device__ __forceinline__ TileOffsets() {
+    using L = KvTile<D, F8>;
+    const int lane = threadIdx.x;
+    const int n = lane & 15, g = lane >> 4;
+    if constexpr (F8) {
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) koff[j] = L::offset(n, 2 * j + (g >> 1)) + 8 * (g & 1);
+      const int s16 = lane & 15;
+#pragma unroll
+      for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(kappa(g, s16 >> 1), blk) + 8 * (s16 & 1);
+    } else {
+#pragma unroll
+      for (int j = 0; j < D / 32; ++j) koff[j] = L::offset(n, 4 * j + g);
+      const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
+#pragma unroll
+      for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
+    }
+  }
+};
+
+// Folds the 32-key tile in `stage` (LDS byte address) whose first key is t0
+// into `st`; keys at or past `te` are masked. qf holds this lane's head's
+// query (zeros for heads past the group), sc the softmax scale times log2(e)
+// (and an fp8 pool's k_scale).
 template <typename T, int D, bool F8>
-__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& lds, const typename Mfma<T>::Frag* qf,
-                                          int seq, int kvh, int kb, int ke, DecodeState& st) {
+__device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const typename Mfma<T>::Frag* qf, float sc,
+                                          const TileOffsets<D, F8>& o, DecodeState& st) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
   using L = KvTile<D, F8>;
   constexpr int kSteps = D / 32;
   const int lane = threadIdx.x;
-  const int n = lane & 15, g = lane >> 4;
-  // Per-lane LDS byte offsets within a tile: the K operand of key n, step j
-  // (key 16 + n sits L::kRow16 bytes below), and the V^T reads' addresses
-  // (li_read_vt's two for 16-bit rows, the one 8-bit transposing read for
-  // fp8 rows; see F8Tile).
-  uint32_t koff[kSteps], voff[D / 16];
-  if constexpr (F8) {
+  const int g = lane >> 4;
+  floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < kSteps; ++j) koff[j] = L::offset(n, 2 * j + (g >> 1)) + 8 * (g & 1);
-    const int s16 = lane & 15;
-#pragma unroll
-    for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(kappa(g, s16 >> 1), blk) + 8 * (s16 & 1);
-  } else {
-#pragma unroll
-    for (int j = 0; j < kSteps; ++j) koff[j] = L::offset(n, 4 * j + g);
-    const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
-#pragma unroll
-    for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
+  for (int j = 0; j < kSteps; ++j) {
+    if constexpr (F8) {
+      s0 = M::mma(lds_read_f8_frag<Frag>(stage + o.koff[j]), qf[j], s0);
+      s1 = M::mma(lds_read_f8_frag<Frag>(stage + o.koff[j] + L::kRow16), qf[j], s1);
+    } else {
+      s0 = M::mma(lds_read_frag<Frag>(stage + o.koff[j]), qf[j], s0);
+      s1 = M::mma(lds_read_frag<Frag>(stage + o.koff[j] + L::kRow16), qf[j], s1);
+    }
   }
+  float x[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    x[r] = s0[r];
+    x[4 + r] = s1[r];
+  }
+  if (t0 + 32 > te) {  // a partial tile: mask the keys past its end
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = (t0 + kappa(g, e) < te) ? x[e] : -INFINITY;
+  }
+  float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
+  mx = fmaxf(fmaxf(mx, x[3]), x[4]);
+  mx = fmaxf(fmaxf(mx, x[5]), fmaxf(x[6], x[7]));
+  mx = li_group_max(mx) * sc;
+  // Lazy rescale (see kLazyRescale).
+  const float mnew = (mx > st.m + kLazyRescale) ? mx : st.m;
+  const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
+  float p[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
+  const float psum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  st.l = st.l * alpha + psum;
+  if (__any(mnew != st.m)) {
+#pragma unroll
+    for (int i = 0; i < D / 16; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.acc[i][r] *= alpha;
+  }
+  st.m = mnew;
+  u32x4_t pw;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
+  const Frag pf = __builtin_bit_cast(Frag, pw);
+  // O^T += V^T P^T, 16 dims at a time, V^T straight out of LDS.
+  const uint32_t vstage = stage + 32 * L::kRowBytes;
+#pragma unroll
+  for (int blk = 0; blk < D / 16; ++blk) {
+    if constexpr (F8) st.acc[blk] = M::mma(lds_read_f8_vt<Frag>(vstage + o.voff[blk]), pf, st.acc[blk]);
+    else st.acc[blk] = M::mma(lds_read_vt<Frag>(vstage + o.voff[blk], vstage + o.voff[blk] + L::kRow16), pf, st.acc[blk]);
+  }
+}
+
+// Folds keys [kb, ke) of sequence `seq`'s context for KV head `kvh` into `st`.
+// qf holds this lane's head's query (zeros for heads past the group).
+template <typename T, int D, bool F8>
+__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& lds, const typename Mfma<T>::Frag* qf,
+                                          int seq, int kvh, int kb, int ke, DecodeState& st) {
+  using L = KvTile<D, F8>;
+  const int lane = threadIdx.x;
+  const TileOffsets<D, F8> off;
   const int esize = F8 ? 1 : (int)sizeof(T);  // bytes per pool element
   const char* kpool = static_cast<const char*>(a.kp) + (int64_t)kvh * a.p_s1 * esize;
   const char* vpool = static_cast<const char*>(a.vp) + (int64_t)kvh * a.p_s1 * esize;
@@ -143,59 +215,8 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& l
       for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
     }
 
-    // Folds the tile in `stage` (LDS byte address) whose first key is t0.
     auto fold = [&](uint32_t stage, int t0) __attribute__((always_inline)) {
-      floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < kSteps; ++j) {
-        if constexpr (F8) {
-          s0 = M::mma(lds_read_f8_frag<Frag>(stage + koff[j]), qf[j], s0);
-          s1 = M::mma(lds_read_f8_frag<Frag>(stage + koff[j] + L::kRow16), qf[j], s1);
-        } else {
-          s0 = M::mma(lds_read_frag<Frag>(stage + koff[j]), qf[j], s0);
-          s1 = M::mma(lds_read_frag<Frag>(stage + koff[j] + L::kRow16), qf[j], s1);
-        }
-      }
-      float x[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = s0[r];
-        x[4 + r] = s1[r];
-      }
-      if (t0 + 32 > c1) {  // a partial tile: mask the keys past the chunk
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = (t0 + kappa(g, e) < c1) ? x[e] : -INFINITY;
-      }
-      float mx = fmaxf(fmaxf(x[0], x[1]), x[2]);
-      mx = fmaxf(fmaxf(mx, x[3]), x[4]);
-      mx = fmaxf(fmaxf(mx, x[5]), fmaxf(x[6], x[7]));
-      mx = li_group_max(mx) * sc;
-      // Lazy rescale (see kLazyRescale).
-      const float mnew = (mx > st.m + kLazyRescale) ? mx : st.m;
-      const float alpha = __builtin_amdgcn_exp2f(st.m - mnew);
-      float p[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) p[e] = __builtin_amdgcn_exp2f(fmaf(x[e], sc, -mnew));
-      const float psum = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-      st.l = st.l * alpha + psum;
-      if (__any(mnew != st.m)) {
-#pragma unroll
-        for (int i = 0; i < D / 16; ++i)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) st.acc[i][r] *= alpha;
-      }
-      st.m = mnew;
-      u32x4_t pw;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>(p[2 * u], p[2 * u + 1]);
-      const Frag pf = __builtin_bit_cast(Frag, pw);
-      // O^T += V^T P^T, 16 dims at a time, V^T straight out of LDS.
-      const uint32_t vstage = stage + 32 * L::kRowBytes;
-#pragma unroll
-      for (int blk = 0; blk < D / 16; ++blk) {
-        if constexpr (F8) st.acc[blk] = M::mma(lds_read_f8_vt<Frag>(vstage + voff[blk]), pf, st.acc[blk]);
-        else st.acc[blk] = M::mma(lds_read_vt<Frag>(vstage + voff[blk], vstage + voff[blk] + L::kRow16), pf, st.acc[blk]);
-      }
+      fold_tile<T, D, F8>(stage, t0, c1, qf, sc, off, st);
     };
 
     // Two stages: while one tile is folded the next tile's loads land in the
@@ -445,6 +466,158 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Head-grouped balanced decode: the balanced split over (sequence, group of
+// HG KV heads, key) instead of (sequence, KV head, key), each wave folding
+// every head of its group: for each 32-key tile, the group's heads one after
+// the other, each into its own online-softmax state. Consecutive tiles of a
+// wave then read HG adjacent rows of the same slots — HG * head_dim * 2
+// contiguous bytes of K (and of V) per slot — which DRAM serves faster than
+// separate per-head streams (a load-only probe of config 2's rows: +5% for
+// all 8 heads together). A (sequence, group) is split at the same keys for
+// each of its heads; a wave's two partial slots hold the group's HG heads
+// (AttnArgs::part_heads = HG).
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool F8, int HG>
+__global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
+  using Frag = typename Mfma<T>::Frag;
+  using L = KvTile<D, F8>;
+  static_assert(HG % 2 == 0, "an even head count keeps every ring stage index a constant");
+  __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds;
+  const float vscale = F8 ? a.v_scale : 1.f;
+  const int lane = threadIdx.x;
+  const int w = blockIdx.x;
+  const int ngroups = a.num_kv_heads / HG;
+  int64_t total;
+  {
+    int64_t t = 0;
+    for (int s0 = 0; s0 < a.batch; s0 += 64) {
+      const int sq = s0 + lane;
+      t += sq < a.batch ? (int64_t)decode_keys(a, sq) : 0;
+    }
+    total = wave_sum_i64(t) * ngroups;
+  }
+  const int64_t share = ((total + a.num_parts - 1) / a.num_parts + 31) / 32 * 32;
+  int64_t pos = (int64_t)w * share;
+  if (pos >= total) return;
+  const int64_t end = min(pos + share, total);
+
+  // The sequence holding flattened key `pos`.
+  int seq = 0;
+  int64_t before = 0;  // flattened keys of the sequences before `seq`
+  for (int s0 = 0; s0 < a.batch; s0 += 64) {
+    const int sq = s0 + lane;
+    const int64_t c = sq < a.batch ? (int64_t)decode_keys(a, sq) * ngroups : 0;
+    int64_t incl = c;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int lo = __shfl_up((int)(incl & 0xffffffff), off, 64);
+      const int hi = __shfl_up((int)(incl >> 32), off, 64);
+      if (lane >= off) incl += ((int64_t)hi << 32) | (uint32_t)lo;
+    }
+    const uint64_t hit = __ballot(before + incl > pos);
+    if (hit) {
+      const int first = __ffsll((long long)hit) - 1;
+      const int64_t excl = __shfl(incl - c, first, 64);
+      seq = s0 + first;
+      before += excl;
+      break;
+    }
+    before += __shfl(incl, 63, 64);
+  }
+
+  const int G = a.groups;
+  const TileOffsets<D, F8> off;
+  const int esize = F8 ? 1 : (int)sizeof(T);
+  const uint32_t row_bytes = (uint32_t)(a.p_s0 * esize);
+  const float sc = a.scale * (F8 ? a.k_scale : 1.f) * kLog2eMfma;
+  const int64_t head_bytes = a.p_s1 * esize;
+  float* part_o = a.part_o + (int64_t)w * 2 * HG * G * a.head_dim;
+  float* part_lse = a.part_lse + (int64_t)w * 2 * HG * G;
+  int ctx = decode_keys(a, seq);
+  int grp, key0;
+  {
+    const int64_t local = pos - before;
+    grp = (int)(local / ctx);
+    key0 = (int)(local - (int64_t)grp * ctx);
+  }
+  bool first_segment = true;
+  while (pos < end) {
+    const int take = (int)min((int64_t)(ctx - key0), end - pos);
+    const int h0 = grp * HG;  // the group's first KV head
+    if (key0 == 0 && lane < HG) {
+      // This wave holds the context's first key: the waves holding its
+      // pieces, for each head of the group.
+      const int64_t offk = before + (int64_t)grp * ctx;
+      a.pieces[(int64_t)seq * a.num_kv_heads + h0 + lane] =
+          int4{w, (int)((offk + ctx - 1) / share), first_segment ? 0 : 1, 0};
+    }
+    const int row = decode_row(a, seq);
+    Frag qf[HG][D / 32];
+    DecodeState st[HG];
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      load_query<T, D>(a, row, h0 + h, qf[h]);
+      reset_state(st[h]);
+    }
+    const char* kbase = static_cast<const char*>(a.kp) + h0 * head_bytes;
+    const char* vbase = static_cast<const char*>(a.vp) + h0 * head_bytes;
+    const int64_t* srow = a.st + (int64_t)seq * a.st_s;
+    const int kb = key0, ke = key0 + take;
+    for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
+      const int c1 = min(c0 + kSlotChunk, ke);
+      const int ntiles = (c1 - c0 + 31) / 32;
+      {
+        int vals[kSlotChunk / 64 + 1];
+#pragma unroll
+        for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
+#pragma unroll
+        for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
+      }
+      // The ring runs over (tile, head) pairs; pair ti * HG + h folds from
+      // stage h % 2 while the next pair's loads land in the other stage.
+      // Past the chunk the look-ahead re-reads a real tile.
+      constexpr int kInFlight = 2 * L::kInsts;
+      issue_tile<D, F8>(lds.stage[0], kbase, vbase, lds.sl, row_bytes, 0, lane);
+      for (int ti = 0; ti < ntiles; ++ti) {
+#pragma unroll
+        for (int h = 0; h < HG; ++h) {
+          const int nh = h + 1 < HG ? h + 1 : 0;
+          const int nt = h + 1 < HG ? ti : ti + 1;
+          issue_tile<D, F8>(lds.stage[(h + 1) & 1], kbase + nh * head_bytes, vbase + nh * head_bytes, lds.sl,
+                            row_bytes, min(32 * nt, kSlotChunk), lane);
+          li_wait_vm<kInFlight>();
+          fold_tile<T, D, F8>(lds_addr(lds.stage[h & 1]), c0 + 32 * ti, c1, qf[h], sc, off, st[h]);
+        }
+      }
+      li_wait_vm<0>();
+    }
+    const bool whole = key0 == 0 && take == ctx;
+    const int slot = first_segment ? 0 : 1;
+#pragma unroll
+    for (int h = 0; h < HG; ++h) {
+      if (whole) {
+        store_state<T, D>(st[h], static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)(h0 + h) * G * a.o_s1,
+                          a.o_s1, nullptr, nullptr, 0, G, vscale);
+      } else {
+        const int64_t r = ((int64_t)slot * HG + h) * G;
+        store_state<T, D>(st[h], nullptr, 0, part_o + r * a.head_dim, part_lse + r, 1, G, vscale);
+      }
+    }
+    pos += take;
+    first_segment = false;
+    key0 = 0;
+    if (++grp == ngroups) {
+      grp = 0;
+      before += (int64_t)ctx * ngroups;
+      ++seq;
+      while (pos < end && seq < a.batch && decode_keys(a, seq) == 0) ++seq;
+      if (seq >= a.batch) break;
+      ctx = decode_keys(a, seq);
+    }
+  }
+}
+
 // Folds the pieces of each (sequence, head) the balanced kernel split across
 // waves: w_p = 2^(lse_p - max lse), out = sum w_p o_p / sum w_p
 // (paged_kernels.py:574-629, in the log2 domain). One wave per (sequence,
@@ -466,7 +639,12 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   const int w0 = info.x, w1 = info.y, slot0 = info.z;
   if (w1 <= w0) return;
   const int n = w1 - w0 + 1;
-  auto row_of = [&](int j) -> int64_t { return ((int64_t)(w0 + j) * 2 + (j == 0 ? slot0 : 0)) * G + h; };
+  // Partial row of piece j: wave w0 + j's slot, then (head-grouped waves)
+  // the KV head within the slot, then the head within the group.
+  const int ph = a.part_heads;
+  auto row_of = [&](int j) -> int64_t {
+    return (((int64_t)(w0 + j) * 2 + (j == 0 ? slot0 : 0)) * ph + kvh % ph) * G + h;
+  };
 
   float mx = -INFINITY;
   for (int j = lane; j < n; j += 64) mx = fmaxf(mx, a.part_lse[row_of(j)]);
@@ -530,10 +708,12 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
   if (blocks == 0) return LI_OK;
   if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "decode grid of %lld blocks is too large", (long long)blocks);
   const dim3 grid((unsigned)blocks), block(64);
-#define LI_DECODE_LAUNCH(T, D, F8)                                                        \
-  do {                                                                                    \
-    if (balanced) hipLaunchKernelGGL((decode_balanced<T, D, F8>), grid, block, 0, s, a);  \
-    else hipLaunchKernelGGL((decode_partitioned<T, D, F8>), grid, block, 0, s, a);        \
+#define LI_DECODE_LAUNCH(T, D, F8)                                                                   \
+  do {                                                                                               \
+    if (!F8 && balanced && a.part_heads == kDecodeHeadGroup)                                         \
+      hipLaunchKernelGGL((decode_grouped<T, D, false, kDecodeHeadGroup>), grid, block, 0, s, a);     \
+    else if (balanced) hipLaunchKernelGGL((decode_balanced<T, D, F8>), grid, block, 0, s, a);        \
+    else hipLaunchKernelGGL((decode_partitioned<T, D, F8>), grid, block, 0, s, a);                   \
   } while (0)
   if (a.kv_fp8) {
     if (dtype == LI_BF16) LI_DECODE_LAUNCH(li_bf16, 128, true);

@@ -41,6 +41,7 @@ struct AttnArgs {
   int max_context;        // slot-table width (prefill)
   int single_query_elsewhere;  // prefill: one-query sequences are served by the decode kernel
   int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
+  int part_heads;  // balanced decode: KV heads per partial slot (1; num_kv_heads when head-grouped)
   int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
   int* queue;    // MFMA prefill: kPrefillQueues unit counters, then the number of blocks listed in `work`
   // fp8 (e4m3) pools: kp / vp hold K / k_scale and V / v_scale, one byte per
@@ -52,6 +53,13 @@ struct AttnArgs {
 
 // Work queues of the persistent MFMA prefill grid (one per XCD).
 constexpr int kPrefillQueues = 8;
+
+// KV heads one wave of the head-grouped balanced decode folds together
+// (when num_kv_heads is a multiple of it).
+#ifndef LI_DECODE_HEAD_GROUP
+#define LI_DECODE_HEAD_GROUP 2
+#endif
+constexpr int kDecodeHeadGroup = LI_DECODE_HEAD_GROUP;
 
 // Largest head_dim the general-shape kernel serves.
 constexpr int kGenericMaxHeadDim = 512;

@@ -33,6 +33,13 @@ int env_int(const char* name, int fallback) {
   return x > 0 ? x : fallback;
 }
 
+// A 0/1 switch from the environment; unset or empty gives `fallback`.
+bool env_flag(const char* name, bool fallback) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return fallback;
+  return std::atoi(v) != 0;
+}
+
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 // Returns the partition count of the grid and the fixed partition length
@@ -79,8 +86,19 @@ int balanced_waves(int num_cus) {
   return std::max(1, num_cus) * per_cu;
 }
 
+// KV heads per partial slot of the balanced split: kDecodeHeadGroup when
+// the head-grouped kernel serves the shape (a 16-bit pool, num_kv_heads a
+// multiple of the group), else one. Grouping pays on 16-bit pools (config 2:
+// 204 -> 196 us) and costs on fp8 ones (config 4: 191 -> 200 us), whose
+// per-head rows are already half as long. LI_DECODE_GROUPED=0 switches it off.
+int balanced_part_heads(int num_kv_heads, bool kv_fp8) {
+  static const bool grouped = env_flag("LI_DECODE_GROUPED", true);
+  return grouped && !kv_fp8 && num_kv_heads % kDecodeHeadGroup == 0 ? kDecodeHeadGroup : 1;
+}
+
 size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads) {
-  const size_t rows = (size_t)waves * 2 * groups;
+  // Sized for either pool type (the plan calls do not know it).
+  const size_t rows = (size_t)waves * 2 * groups * balanced_part_heads(num_kv_heads, false);
   return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) +
          align256((size_t)batch * num_kv_heads * 16);
 }
@@ -89,7 +107,8 @@ size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int nu
 void set_balanced(AttnArgs& d, int waves, void* workspace) {
   d.num_parts = waves;
   d.part_len = -1;
-  const size_t rows = (size_t)waves * 2 * d.groups;
+  d.part_heads = balanced_part_heads(d.num_kv_heads, d.kv_fp8 != 0);
+  const size_t rows = (size_t)waves * 2 * d.groups * d.part_heads;
   char* p = static_cast<char*>(workspace);
   d.part_o = reinterpret_cast<float*>(p);
   p += align256(rows * d.head_dim * sizeof(float));
