@@ -28,7 +28,9 @@
 //
 // Every LDS read is one instruction from a per-lane address fixed for the
 // whole kernel plus an immediate offset (the loop body covers both stages,
-// so stage bases are constants).
+// so stage bases are constants); a tile's V^T fragments, and the next key
+// block's K fragments, are read as one batch ahead of the MFMAs that
+// consume them, so the LDS latency is paid once per batch.
 //
 // A row's visibility is key <= its position; the mask is a compare per
 // score, applied only to stages that reach past the block's first query
@@ -37,7 +39,7 @@
 // wave whose rows are all padding only helps load the stages.
 //
 // Scheduling: a persistent grid of one work-group per CU. prefill_order
-// lists every non-empty query block, heaviest first; work-groups pull
+// lists every non-empty query block, by sequence, heaviest first; work-groups pull
 // (block, KV head) units from queues in that order through an atomic
 // counter, so long units start first, short ones fill in behind, and no
 // work-group is launched for an empty block. With num_kv_heads a multiple of
@@ -57,6 +59,9 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kMinRows = 32 * kWaves;  // rows of a work-group
 constexpr int kStageKeys = 64;
+// Keeps the compiler from moving instructions across this point (so a batch
+// of LDS reads stays ahead of the MFMAs that consume it).
+#define LI_SCHED_FENCE() __builtin_amdgcn_sched_barrier(0)
 
 // Issues this wave's share of the direct-to-LDS loads of the 64 keys whose
 // first key is entry `t` of the staged slots. The stage takes 2 * kInsts
@@ -64,7 +69,7 @@ constexpr int kStageKeys = 64;
 // pairs p = w * kPer .. w * kPer + kPer - 1, pair p being instruction
 // p % kInsts of half p / kInsts.
 template <typename L, int W>
-__device__ __forceinline__ void issue_stage(char* stage, const char* __restrict__ kpool,
+__device__ __forceinline__ void issue_stage(uint32_t stage, const char* __restrict__ kpool,
                                             const char* __restrict__ vpool, const int* __restrict__ sl,
                                             uint32_t row_bytes, int t, int lane, int w) {
   constexpr int kPer = 2 * L::kInsts / W;
@@ -82,7 +87,7 @@ __device__ __forceinline__ void issue_stage(char* stage, const char* __restrict_
   for (int ii = 0; ii < kPer; ++ii) {
     const int p = w * kPer + ii, half = p / L::kInsts, i = p % L::kInsts;
     const int key = rr * L::kInsts + i;
-    const uint32_t dst = lds_addr(stage + half * L::kTileBytes + i * 1024);
+    const uint32_t dst = stage + half * L::kTileBytes + i * 1024;
     // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
     dma16(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), slot[ii], row_bytes), dst);
     dma16(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), dst + 32 * L::kRowBytes);
@@ -242,33 +247,43 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     for (int blk = 0; blk < D / 16; ++blk) voff[blk] = base + L::voffset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
   }
 
-  // Folds the 64 keys of stage S (first key t0) into both row blocks: scores
-  // of all 64 keys, one softmax update per row block, then P V.
-  auto fold = [&](auto stage_tag, int t0) __attribute__((always_inline)) {
-    constexpr int S = decltype(stage_tag)::value;
-    constexpr uint32_t kStage = S * 2 * L::kTileBytes;
+  // The fold of one 64-key stage in three parts: scores (MFMA), the online
+  // softmax (VALU), P V (MFMA). `sb` is the stage's byte offset from
+  // stages[0]; the per-lane offsets add it once per part.
+  //
+  // qk: s[nb][b], lane (n, g) holds the scores of keys 16 b + 4 g + r, r < 4,
+  // of row n of block nb.
+  auto qk = [&](uint32_t sb, floatx4_t (&s)[2][4]) __attribute__((always_inline)) {
     constexpr uint32_t kRow16 = L::kRow16;
-    // s[nb][b]: lane (n, g) holds the scores of keys 16 b + 4 g + r, r < 4,
-    // of row n of block nb.
-    floatx4_t s[2][4];
-    __builtin_amdgcn_s_setprio(1);
+    uint32_t ko[kSteps];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) ko[j] = koff[j] + sb;
+    // Key block b + 1's K fragments load while block b's MFMAs run.
+    Frag kf[2][kSteps];
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) kf[0][j] = lds_read_frag<Frag>(ko[j]);
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const uint32_t tb = kStage + (b >> 1) * L::kTileBytes + (b & 1) * kRow16;
-      Frag kf[kSteps];
+      if (b + 1 < 4) {
+        const uint32_t tb = ((b + 1) >> 1) * L::kTileBytes + ((b + 1) & 1) * kRow16;
 #pragma unroll
-      for (int j = 0; j < kSteps; ++j) kf[j] = lds_read_frag<Frag>(koff[j] + tb);
+        for (int j = 0; j < kSteps; ++j) kf[(b + 1) & 1][j] = lds_read_frag<Frag>(ko[j] + tb);
+      }
+      LI_SCHED_FENCE();
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        s[nb][b] = M::mma(kf[0], qf[nb][0], floatx4_t{0.f, 0.f, 0.f, 0.f});
+        s[nb][b] = M::mma(kf[b & 1][0], qf[nb][0], floatx4_t{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-        for (int j = 1; j < kSteps; ++j) s[nb][b] = M::mma(kf[j], qf[nb][j], s[nb][b]);
+        for (int j = 1; j < kSteps; ++j) s[nb][b] = M::mma(kf[b & 1][j], qf[nb][j], s[nb][b]);
       }
+      LI_SCHED_FENCE();
     }
-    __builtin_amdgcn_s_setprio(0);
-    // Online softmax per row block over the stage's 64 keys; the scale is
-    // folded into the exponent.
-    Frag pf[2][2];
+  };
+  // softmax: one running-max update per row block over the stage's 64 keys
+  // (first key t0), the scale folded into the exponent; the weights, rounded
+  // to T, into pf[nb][t] (32-key tile t), the accumulator rescaled when the
+  // maximum moved.
+  auto softmax = [&](int t0, floatx4_t (&s)[2][4], Frag (&pf)[2][2]) __attribute__((always_inline)) {
     float alpha[2];
     bool rescale = false;
     const bool masked = t0 + kStageKeys - 1 > lim_lo;  // reaches past some row's last key
@@ -320,21 +335,43 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 #pragma unroll
           for (int r = 0; r < 4; ++r) acc[nb][i][r] *= alpha[nb];
     }
-    __builtin_amdgcn_s_setprio(1);
-    // O^T += V^T P^T, 16 dims at a time, for each 32-key tile of the stage.
+  };
+  // pv: O^T += V^T P^T, 16 dims at a time, for each 32-key tile of the stage.
+  auto pv = [&](uint32_t sb, const Frag (&pf)[2][2]) __attribute__((always_inline)) {
+    constexpr uint32_t kRow16 = L::kRow16;
+    constexpr uint32_t kV = 32 * L::kRowBytes;
+    uint32_t vo[D / 16];
+#pragma unroll
+    for (int blk = 0; blk < D / 16; ++blk) vo[blk] = voff[blk] + sb + kV;
+    // A tile's eight V^T fragments load together, then its MFMAs run.
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      constexpr uint32_t kV = 32 * L::kRowBytes;
-      const uint32_t tb = kStage + t * L::kTileBytes + kV;
+      const uint32_t tb = t * L::kTileBytes;
+      Frag vf[D / 16];
 #pragma unroll
-      for (int blk = 0; blk < D / 16; ++blk) {
-        const Frag vf = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + kRow16);
+      for (int blk = 0; blk < D / 16; ++blk) vf[blk] = lds_read_vt<Frag>(vo[blk] + tb, vo[blk] + tb + kRow16);
+      LI_SCHED_FENCE();
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf, pf[nb][t], acc[nb][blk]);
-      }
+      for (int blk = 0; blk < D / 16; ++blk)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf[blk], pf[nb][t], acc[nb][blk]);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) acc[nb][D / 16] = M::mma(ones, pf[nb][t], acc[nb][D / 16]);
+      LI_SCHED_FENCE();
     }
+  };
+  // One stage: the three parts back to back, the MFMA parts at raised wave
+  // priority so a SIMD issues them ahead of the other wave's softmax.
+  auto fold = [&](auto stage_tag, int t0) __attribute__((always_inline)) {
+    constexpr uint32_t sb = decltype(stage_tag)::value * 2 * L::kTileBytes;
+    floatx4_t s[2][4];
+    Frag pf[2][2];
+    __builtin_amdgcn_s_setprio(1);
+    qk(sb, s);
+    __builtin_amdgcn_s_setprio(0);
+    softmax(t0, s, pf);
+    __builtin_amdgcn_s_setprio(1);
+    pv(sb, pf);
     __builtin_amdgcn_s_setprio(0);
   };
 
@@ -354,15 +391,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
     // every wave has the same loads in flight at every wait. The loop body
     // handles both stages so that each stage's LDS offsets are constants.
     if constexpr (!F8) {
-      issue_stage<LS, W>(stages[0], kpool, vpool, sl, row_bytes, 0, lane, w);
+      // Two stages: the next 64 keys land in one while the other is folded.
+      // Past the chunk the look-ahead re-reads a real stage (cache hits), so
+      // every wave has the same loads in flight at every wait. The loop body
+      // handles both stages so that each stage's LDS offsets are constants.
+      issue_stage<LS, W>(lds_addr(stages[0]), kpool, vpool, sl, row_bytes, 0, lane, w);
       for (int ti = 0; ti < ntiles; ti += 2) {
-        issue_stage<LS, W>(stages[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
+        issue_stage<LS, W>(lds_addr(stages[1]), kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
         li_wait_vm<kDmaPerStage>();
         __syncthreads();
         if (!idle) fold(Stage0{}, c0 + kStageKeys * ti);
         __syncthreads();
         if (ti + 1 >= ntiles) break;
-        issue_stage<LS, W>(stages[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
+        issue_stage<LS, W>(lds_addr(stages[0]), kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
         li_wait_vm<kDmaPerStage>();
         __syncthreads();
         if (!idle) fold(Stage1{}, c0 + kStageKeys * (ti + 1));
@@ -374,16 +415,16 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
       // barrier the waves fold stages[x]. raw[x] takes its next loads once
       // converted; stages[x] is converted again only after every wave has
       // passed the barrier of the stage in between, so after its fold.
-      issue_stage<LS, W>(raw[0], kpool, vpool, sl, row_bytes, 0, lane, w);
+      issue_stage<LS, W>(lds_addr(raw[0]), kpool, vpool, sl, row_bytes, 0, lane, w);
       for (int ti = 0; ti < ntiles; ti += 2) {
-        issue_stage<LS, W>(raw[1], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
+        issue_stage<LS, W>(lds_addr(raw[1]), kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
         li_wait_vm<kDmaPerStage>();
         __syncthreads();
         convert_stage<T, W>(lds_addr(raw[0]), lds_addr(stages[0]), tid);
         __syncthreads();
         if (!idle) fold(Stage0{}, c0 + kStageKeys * ti);
         if (ti + 1 >= ntiles) break;
-        issue_stage<LS, W>(raw[0], kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
+        issue_stage<LS, W>(lds_addr(raw[0]), kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
         li_wait_vm<kDmaPerStage>();
         __syncthreads();
         convert_stage<T, W>(lds_addr(raw[1]), lds_addr(stages[1]), tid);
@@ -413,45 +454,54 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 }
 
 // Work list of the prefill grid: every non-empty query block
-// (sequence * num_qblocks + block) ordered by the number of 32-key tiles it
-// folds, most first (a counting sort on tiles >> shift), then -1 up to
-// batch * num_qblocks. Work-groups are dispatched in grid order as earlier
-// ones retire, so this is longest-processing-time-first scheduling: the
-// long blocks start at once and the short ones fill in behind them. One
-// work-group; the order within a bucket is whatever the LDS atomics give,
-// which changes the schedule only, never a result.
+// (sequence * num_qblocks + block), a sequence's blocks side by side, last
+// (heaviest) block first, the sequences ordered by the 32-key tiles of their
+// heaviest block, most first (a counting sort on tiles >> shift), then -1 up
+// to batch * num_qblocks. Work-groups take units in this order as earlier
+// ones retire, so the long blocks start at once and the short ones fill in
+// behind them (longest-processing-time-first, by sequence), and the
+// work-groups running at one time on an XCD fold blocks of one sequence:
+// they sweep the same keys at about the same pace, so each K/V tile comes
+// from HBM once into that XCD's L2 and is read there by the rest. One
+// work-group; the order of sequences within a bucket is whatever the LDS
+// atomics give, which changes the schedule only, never a result.
 constexpr int kOrderBins = 256;
 
 __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   __shared__ int hist[kOrderBins];
   __shared__ int max_tiles;
   const int tid = threadIdx.x;
-  const int items = a.batch * a.num_qblocks;
-  auto tiles_of = [&](int it) {
-    const int seq = it / a.num_qblocks, qb = it % a.num_qblocks;
+  // Blocks of sequence `seq` the prefill folds, and the tiles of its
+  // heaviest (last) block.
+  auto blocks_of = [&](int seq, int* tiles) {
     const int first = a.qsl[seq];
     const int nq = a.qsl[seq + 1] - first;
-    const int q0 = qb * a.block_q;
-    if (q0 >= nq || (nq == 1 && a.single_query_elsewhere)) return 0;
-    const int kend = a.ctx[seq] - nq + min(q0 + a.block_q, nq);
-    return (kend + 31) / 32;
+    *tiles = 0;
+    if (nq <= 0 || (nq == 1 && a.single_query_elsewhere)) return 0;
+    *tiles = (a.ctx[seq] + 31) / 32;
+    return min((nq + a.block_q - 1) / a.block_q, a.num_qblocks);
   };
   if (tid < kOrderBins) hist[tid] = 0;
   if (tid == 0) max_tiles = 0;
   __syncthreads();
   int local = 0;
-  for (int it = tid; it < items; it += 1024) local = max(local, tiles_of(it));
+  for (int sq = tid; sq < a.batch; sq += 1024) {
+    int t;
+    blocks_of(sq, &t);
+    local = max(local, t);
+  }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) local = max(local, __shfl_xor(local, off, 64));
   if ((tid & 63) == 0) atomicMax(&max_tiles, local);
   __syncthreads();
   int shift = 0;
   while ((max_tiles >> shift) >= kOrderBins) ++shift;
-  // Bin b holds blocks of (tiles >> shift) == kOrderBins - 1 - b, so bins
-  // run from the heaviest down.
-  for (int it = tid; it < items; it += 1024) {
-    const int t = tiles_of(it);
-    if (t > 0) atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], 1);
+  // Bin b holds the blocks of sequences with (tiles >> shift) ==
+  // kOrderBins - 1 - b, so bins run from the heaviest down.
+  for (int sq = tid; sq < a.batch; sq += 1024) {
+    int t;
+    const int nb = blocks_of(sq, &t);
+    if (nb > 0) atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
   }
   __syncthreads();
   // Exclusive prefix sum over the bins: Hillis-Steele in LDS.
@@ -469,10 +519,14 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   if (tid < kOrderBins) hist[tid] = v - own;
   if (tid == kOrderBins - 1) max_tiles = v;  // now: the number of blocks listed
   __syncthreads();
-  for (int it = tid; it < items; it += 1024) {
-    const int t = tiles_of(it);
-    if (t > 0) a.work[atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], 1)] = it;
+  for (int sq = tid; sq < a.batch; sq += 1024) {
+    int t;
+    const int nb = blocks_of(sq, &t);
+    if (nb == 0) continue;
+    const int at = atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
+    for (int i = 0; i < nb; ++i) a.work[at + i] = sq * a.num_qblocks + (nb - 1 - i);
   }
+  const int items = a.batch * a.num_qblocks;
   for (int i = max_tiles + tid; i < items; i += 1024) a.work[i] = -1;
   // The persistent grid's queues start empty for this launch.
   if (tid < kPrefillQueues) a.queue[tid] = 0;
