@@ -142,3 +142,16 @@ def test_long_context_is_partitioned_and_combined():
     b = PagedBatch([20000, 3000], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128,
                    num_slots=32768, seed=9)
     assert_within(_run(b), b.oracle(), 2e-2, 2e-3)
+
+
+@pytest.mark.parametrize(("num_heads", "num_kv_heads", "head_dim"), [(32, 8, 128), (16, 1, 64), (12, 6, 128)])
+def test_more_sequences_than_a_wave_has_lanes(num_heads, num_kv_heads, head_dim):
+    """150 sequences: the balanced kernels find a wave's first sequence and
+    count keys 64 sequences at a time, so this takes three passes; some
+    contexts are shorter than a share, some span several waves. KV heads in
+    pairs (8, 6) run the head-grouped kernel, a single KV head the per-head one."""
+    rng = np.random.default_rng(31)
+    ctx = rng.integers(1, 600, size=150).tolist()
+    b = PagedBatch(ctx, dtype=torch.bfloat16, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                   num_slots=8192, seed=31)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)

@@ -116,3 +116,19 @@ def test_persistent_grid_takes_every_unit_on_every_call(num_heads, num_kv_heads)
     for _ in range(3):
         again = _run(b)
         assert torch.equal(again, first)
+
+
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (16, 4)])
+def test_more_sequences_than_the_work_list_kernel_has_threads(num_heads, num_kv_heads):
+    """1,100 sequences (one to three queries each over short prefixes): the
+    work-list kernel walks them in strides of its 1,024 threads, keeps each
+    sequence's blocks together, and the one-query ones go to the decode
+    kernel; Hkv 4 runs the single-queue grid."""
+    rng = np.random.default_rng(21)
+    n = 1100
+    q = rng.integers(1, 4, size=n).tolist()
+    p = rng.integers(0, 40, size=n).tolist()
+    b = PagedBatch([qq + pp for qq, pp in zip(q, p)], q, dtype=torch.bfloat16, num_heads=num_heads,
+                   num_kv_heads=num_kv_heads, head_dim=128, num_slots=65536, seed=21)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+    assert_within(_run(b, one_query_rows=False), b.oracle(), 2 ** -6, 2e-3)
