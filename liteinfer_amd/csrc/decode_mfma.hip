@@ -634,8 +634,11 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   const int seq = blockIdx.x / a.num_heads;
   const int G = a.groups, D = a.head_dim;
   const int kvh = head / G, h = head % G;
-  if (decode_keys(a, seq) == 0) return;
+  // The context length and the piece table are independent loads; both are
+  // issued before either is used.
+  const int keys = decode_keys(a, seq);
   const int4 info = a.pieces[(int64_t)seq * a.num_kv_heads + kvh];
+  if (keys == 0) return;
   const int w0 = info.x, w1 = info.y, slot0 = info.z;
   if (w1 <= w0) return;
   const int n = w1 - w0 + 1;
@@ -645,6 +648,42 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   auto row_of = [&](int j) -> int64_t {
     return (((int64_t)(w0 + j) * 2 + (j == 0 ? slot0 : 0)) * ph + kvh % ph) * G + h;
   };
+
+  const int row = decode_row(a, seq);
+  T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head * a.o_s1;
+  if (n <= kBatch) {
+    // At most kBatch pieces (the usual case): every piece's LSE and partial
+    // row load at once, so the fold waits for one round trip, not two.
+    const float lse = lane < n ? a.part_lse[row_of(lane)] : -INFINITY;
+    float v[kBatch][kMaxC];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const float* po = a.part_o + row_of(min(k, n - 1)) * D;
+#pragma unroll
+      for (int c = 0; c < kMaxC; ++c) {
+        const int d = lane + 64 * c;
+        v[k][c] = (k < n && d < D) ? po[d] : 0.f;
+      }
+    }
+    const float mx = li_wave_max(lse);
+    const float wl = lane < n ? exp2f(lse - mx) : 0.f;
+    const float inv = 1.f / li_wave_sum(wl);
+    float acc[kMaxC];
+#pragma unroll
+    for (int c = 0; c < kMaxC; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const float wt = __shfl(wl, k, 64);
+#pragma unroll
+      for (int c = 0; c < kMaxC; ++c) acc[c] = fmaf(wt, v[k][c], acc[c]);
+    }
+#pragma unroll
+    for (int c = 0; c < kMaxC; ++c) {
+      const int d = lane + 64 * c;
+      if (d < D) orow[d] = li_from_float<T>(acc[c] * inv);
+    }
+    return;
+  }
 
   float mx = -INFINITY;
   for (int j = lane; j < n; j += 64) mx = fmaxf(mx, a.part_lse[row_of(j)]);
@@ -677,8 +716,6 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
     }
   }
   const float inv = 1.f / wsum;
-  const int row = decode_row(a, seq);
-  T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head * a.o_s1;
 #pragma unroll
   for (int c = 0; c < kMaxC; ++c) {
     const int d = lane + 64 * c;
