@@ -488,26 +488,36 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
   const int lane = threadIdx.x;
   const int w = blockIdx.x;
   const int ngroups = a.num_kv_heads / HG;
+  // Work is counted in units: a segment (sequence, group of HG KV heads)
+  // of c keys is ceil(c / 32) tiles plus a.seg_cost units for starting it
+  // (its query, its slots, the ring's first tile), the latter first. Every
+  // wave takes an equal run of units, so a wave that meets more segments
+  // folds fewer tiles, and pieces start and end on tile boundaries.
+  const int R = a.seg_cost;
+  auto units_of = [&](int sq) -> int64_t {
+    const int c = decode_keys(a, sq);
+    return c > 0 ? (int64_t)((c + 31) / 32 + R) : 0;
+  };
   int64_t total;
   {
     int64_t t = 0;
     for (int s0 = 0; s0 < a.batch; s0 += 64) {
       const int sq = s0 + lane;
-      t += sq < a.batch ? (int64_t)decode_keys(a, sq) : 0;
+      t += sq < a.batch ? units_of(sq) : 0;
     }
     total = wave_sum_i64(t) * ngroups;
   }
-  const int64_t share = ((total + a.num_parts - 1) / a.num_parts + 31) / 32 * 32;
+  const int64_t share = (total + a.num_parts - 1) / a.num_parts;
   int64_t pos = (int64_t)w * share;
   if (pos >= total) return;
   const int64_t end = min(pos + share, total);
 
-  // The sequence holding flattened key `pos`.
+  // The sequence holding flattened unit `pos`.
   int seq = 0;
-  int64_t before = 0;  // flattened keys of the sequences before `seq`
+  int64_t before = 0;  // flattened units of the sequences before `seq`
   for (int s0 = 0; s0 < a.batch; s0 += 64) {
     const int sq = s0 + lane;
-    const int64_t c = sq < a.batch ? (int64_t)decode_keys(a, sq) * ngroups : 0;
+    const int64_t c = sq < a.batch ? units_of(sq) * ngroups : 0;
     int64_t incl = c;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -535,85 +545,94 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
   float* part_o = a.part_o + (int64_t)w * 2 * HG * G * a.head_dim;
   float* part_lse = a.part_lse + (int64_t)w * 2 * HG * G;
   int ctx = decode_keys(a, seq);
-  int grp, key0;
+  int nu = (ctx + 31) / 32 + R;  // units of each of the sequence's segments
+  int grp, u0;
   {
     const int64_t local = pos - before;
-    grp = (int)(local / ctx);
-    key0 = (int)(local - (int64_t)grp * ctx);
+    grp = (int)(local / nu);
+    u0 = (int)(local - (int64_t)grp * nu);
   }
   bool first_segment = true;
   while (pos < end) {
-    const int take = (int)min((int64_t)(ctx - key0), end - pos);
-    const int h0 = grp * HG;  // the group's first KV head
-    if (key0 == 0 && lane < HG) {
-      // This wave holds the context's first key: the waves holding its
-      // pieces, for each head of the group.
-      const int64_t offk = before + (int64_t)grp * ctx;
-      a.pieces[(int64_t)seq * a.num_kv_heads + h0 + lane] =
-          int4{w, (int)((offk + ctx - 1) / share), first_segment ? 0 : 1, 0};
-    }
-    const int row = decode_row(a, seq);
-    Frag qf[HG][D / 32];
-    DecodeState st[HG];
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      load_query<T, D>(a, row, h0 + h, qf[h]);
-      reset_state(st[h]);
-    }
-    const char* kbase = static_cast<const char*>(a.kp) + h0 * head_bytes;
-    const char* vbase = static_cast<const char*>(a.vp) + h0 * head_bytes;
-    const int64_t* srow = a.st + (int64_t)seq * a.st_s;
-    const int kb = key0, ke = key0 + take;
-    for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
-      const int c1 = min(c0 + kSlotChunk, ke);
-      const int ntiles = (c1 - c0 + 31) / 32;
-      {
-        int vals[kSlotChunk / 64 + 1];
-#pragma unroll
-        for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
-#pragma unroll
-        for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
+    // Units [u0, u1) of this segment are this wave's; its tiles are units
+    // R .. nu - 1.
+    const int u1 = (int)min((int64_t)nu, (int64_t)u0 + (end - pos));
+    const int t_lo = max(u0 - R, 0), t_hi = u1 - R;
+    if (t_hi > t_lo) {
+      const int key0 = 32 * t_lo;
+      const int take = min(32 * t_hi, ctx) - key0;
+      const int h0 = grp * HG;  // the group's first KV head
+      if (t_lo == 0 && lane < HG) {
+        // This wave holds the context's first key: the waves holding its
+        // pieces, for each head of the group.
+        const int64_t seg = before + (int64_t)grp * nu;
+        a.pieces[(int64_t)seq * a.num_kv_heads + h0 + lane] =
+            int4{w, (int)((seg + nu - 1) / share), first_segment ? 0 : 1, 0};
       }
-      // The ring runs over (tile, head) pairs; pair ti * HG + h folds from
-      // stage h % 2 while the next pair's loads land in the other stage.
-      // Past the chunk the look-ahead re-reads a real tile.
-      constexpr int kInFlight = 2 * L::kInsts;
-      issue_tile<D, F8>(lds.stage[0], kbase, vbase, lds.sl, row_bytes, 0, lane);
-      for (int ti = 0; ti < ntiles; ++ti) {
+      const int row = decode_row(a, seq);
+      Frag qf[HG][D / 32];
+      DecodeState st[HG];
 #pragma unroll
-        for (int h = 0; h < HG; ++h) {
-          const int nh = h + 1 < HG ? h + 1 : 0;
-          const int nt = h + 1 < HG ? ti : ti + 1;
-          issue_tile<D, F8>(lds.stage[(h + 1) & 1], kbase + nh * head_bytes, vbase + nh * head_bytes, lds.sl,
-                            row_bytes, min(32 * nt, kSlotChunk), lane);
-          li_wait_vm<kInFlight>();
-          fold_tile<T, D, F8>(lds_addr(lds.stage[h & 1]), c0 + 32 * ti, c1, qf[h], sc, off, st[h]);
+      for (int h = 0; h < HG; ++h) {
+        load_query<T, D>(a, row, h0 + h, qf[h]);
+        reset_state(st[h]);
+      }
+      const char* kbase = static_cast<const char*>(a.kp) + h0 * head_bytes;
+      const char* vbase = static_cast<const char*>(a.vp) + h0 * head_bytes;
+      const int64_t* srow = a.st + (int64_t)seq * a.st_s;
+      const int kb = key0, ke = key0 + take;
+      for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
+        const int c1 = min(c0 + kSlotChunk, ke);
+        const int ntiles = (c1 - c0 + 31) / 32;
+        {
+          int vals[kSlotChunk / 64 + 1];
+#pragma unroll
+          for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
+#pragma unroll
+          for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
+        }
+        // The ring runs over (tile, head) pairs; pair ti * HG + h folds from
+        // stage h % 2 while the next pair's loads land in the other stage.
+        // Past the chunk the look-ahead re-reads a real tile.
+        constexpr int kInFlight = 2 * L::kInsts;
+        issue_tile<D, F8>(lds.stage[0], kbase, vbase, lds.sl, row_bytes, 0, lane);
+        for (int ti = 0; ti < ntiles; ++ti) {
+#pragma unroll
+          for (int h = 0; h < HG; ++h) {
+            const int nh = h + 1 < HG ? h + 1 : 0;
+            const int nt = h + 1 < HG ? ti : ti + 1;
+            issue_tile<D, F8>(lds.stage[(h + 1) & 1], kbase + nh * head_bytes, vbase + nh * head_bytes, lds.sl,
+                              row_bytes, min(32 * nt, kSlotChunk), lane);
+            li_wait_vm<kInFlight>();
+            fold_tile<T, D, F8>(lds_addr(lds.stage[h & 1]), c0 + 32 * ti, c1, qf[h], sc, off, st[h]);
+          }
+        }
+        li_wait_vm<0>();
+      }
+      const bool whole = key0 == 0 && take == ctx;
+      const int slot = first_segment ? 0 : 1;
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
+        if (whole) {
+          store_state<T, D>(st[h], static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)(h0 + h) * G * a.o_s1,
+                            a.o_s1, nullptr, nullptr, 0, G, vscale);
+        } else {
+          const int64_t r = ((int64_t)slot * HG + h) * G;
+          store_state<T, D>(st[h], nullptr, 0, part_o + r * a.head_dim, part_lse + r, 1, G, vscale);
         }
       }
-      li_wait_vm<0>();
+      first_segment = false;
     }
-    const bool whole = key0 == 0 && take == ctx;
-    const int slot = first_segment ? 0 : 1;
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      if (whole) {
-        store_state<T, D>(st[h], static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)(h0 + h) * G * a.o_s1,
-                          a.o_s1, nullptr, nullptr, 0, G, vscale);
-      } else {
-        const int64_t r = ((int64_t)slot * HG + h) * G;
-        store_state<T, D>(st[h], nullptr, 0, part_o + r * a.head_dim, part_lse + r, 1, G, vscale);
-      }
-    }
-    pos += take;
-    first_segment = false;
-    key0 = 0;
+    pos += u1 - u0;
+    u0 = 0;
     if (++grp == ngroups) {
       grp = 0;
-      before += (int64_t)ctx * ngroups;
+      before += (int64_t)nu * ngroups;
       ++seq;
       while (pos < end && seq < a.batch && decode_keys(a, seq) == 0) ++seq;
       if (seq >= a.batch) break;
       ctx = decode_keys(a, seq);
+      nu = (ctx + 31) / 32 + R;
     }
   }
 }

@@ -41,7 +41,8 @@ struct AttnArgs {
   int max_context;        // slot-table width (prefill)
   int single_query_elsewhere;  // prefill: one-query sequences are served by the decode kernel
   int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
-  int part_heads;  // balanced decode: KV heads per partial slot (1; num_kv_heads when head-grouped)
+  int part_heads;  // balanced decode: KV heads per partial slot (1; kDecodeHeadGroup when head-grouped)
+  int seg_cost;    // head-grouped decode: work units charged per segment start, on top of its 32-key tiles
   int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
   int* queue;    // MFMA prefill: kPrefillQueues unit counters, then the number of blocks listed in `work`
   // fp8 (e4m3) pools: kp / vp hold K / k_scale and V / v_scale, one byte per

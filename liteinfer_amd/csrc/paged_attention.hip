@@ -80,6 +80,7 @@ size_t decode_workspace(int batch, int num_heads, int head_dim, int parts) {
 // flattened key space into equal shares; each wave keeps up to two fp32
 // partials of `groups` heads.
 constexpr int kBalancedWavesPerCu = 4;
+constexpr int kSegmentCost = 2;
 
 int balanced_waves(int num_cus) {
   static const int per_cu = env_int("LI_DECODE_BALANCED_WAVES_PER_CU", kBalancedWavesPerCu);
@@ -96,6 +97,18 @@ int balanced_part_heads(int num_kv_heads, bool kv_fp8) {
   return grouped && !kv_fp8 && num_kv_heads % kDecodeHeadGroup == 0 ? kDecodeHeadGroup : 1;
 }
 
+// What starting a segment (its query, its slots, the ring's first tile)
+// costs the head-grouped decode, in 32-key tiles: the balanced split charges
+// it so that waves meeting many short contexts take fewer tiles.
+// LI_DECODE_SEGMENT_COST overrides it (0 and up).
+int segment_cost() {
+  static const int cost = [] {
+    const char* v = std::getenv("LI_DECODE_SEGMENT_COST");
+    return (v && *v) ? std::max(0, std::atoi(v)) : kSegmentCost;
+  }();
+  return cost;
+}
+
 size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads) {
   // Sized for either pool type (the plan calls do not know it).
   const size_t rows = (size_t)waves * 2 * groups * balanced_part_heads(num_kv_heads, false);
@@ -108,6 +121,7 @@ void set_balanced(AttnArgs& d, int waves, void* workspace) {
   d.num_parts = waves;
   d.part_len = -1;
   d.part_heads = balanced_part_heads(d.num_kv_heads, d.kv_fp8 != 0);
+  d.seg_cost = segment_cost();
   const size_t rows = (size_t)waves * 2 * d.groups * d.part_heads;
   char* p = static_cast<char*>(workspace);
   d.part_o = reinterpret_cast<float*>(p);
