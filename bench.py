@@ -10,7 +10,7 @@ before the clock starts.
 `value` is algorithmic bytes per step / step time, in GB/s: every context
 token's K and V rows for all KV heads plus its int64 slot index, the queries
 and outputs, and the slot-write's reads and writes. `roofline` rates the
-decode call (the partition kernel plus the partition combine, timed with HIP
+decode call (the decode kernel plus its combine, timed with HIP
 events on the stream they run on) against MI355X's 8 TB/s. Config 3's packed
 prefill (TFLOP/s of visible causal pairs; also its 8 chunks alone, its 56
 one-query rows alone in GB/s, and 8 chunks of 2048 queries over 8192 cached
