@@ -184,13 +184,52 @@ def _paged_decode_step(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_
     return out.unsqueeze(2)
 
 
+# Rates the choice below uses (measured on MI355X): the decode kernel streams
+# K/V at about 6 TB/s, the prefill kernel folds about 1 PFLOP/s of visible
+# pairs. The prefill kernel folds a one-query sequence's whole context in one
+# work-group, so it takes them only when contexts are bounded.
+_DECODE_BYTES_PER_S = 6e12
+_PREFILL_FLOPS_PER_S = 1e15
+_LONGEST_ROW_FOR_PREFILL = 8192
+
+
+def _one_query_rows_to_decode_kernel(query_lens, context_lens, num_heads: int, num_kv_heads: int, head_dim: int,
+                                     pool_element_size: int) -> bool:
+    """Whether a packed pass's one-query sequences should go to the decode kernel.
+
+    False (the prefill kernel serves them beside the chunks, in one launch)
+    when there are none, or when streaming their keys takes less than half
+    the time the chunks' MFMA work does and no context is longer than
+    ``_LONGEST_ROW_FOR_PREFILL``: their loads then fill in behind the chunks'
+    units (config 3: 430-441 -> 420 us). Otherwise, and always on fp8 pools,
+    the decode kernel's split over the whole grid serves them (a
+    decode-heavy pass: 644 -> 629 us).
+    The answer is the same either way.
+    """
+    rows = [c for q, c in zip(query_lens, context_lens) if q == 1]
+    if not rows:
+        return False
+    if pool_element_size < 2 or max(rows) > _LONGEST_ROW_FOR_PREFILL:
+        # fp8 pools: every prefill stage also converts in LDS, which the
+        # one-query rows' stages pay too (config 3: 394 -> 404 us in-kernel).
+        return True
+    row_bytes = sum(rows) * num_kv_heads * head_dim * pool_element_size * 2
+    chunk_flops = sum(4 * num_heads * head_dim * (q * (c - q) + q * (q + 1) / 2)
+                      for q, c in zip(query_lens, context_lens) if q > 1)
+    return row_bytes / _DECODE_BYTES_PER_S > 0.5 * chunk_flops / _PREFILL_FLOPS_PER_S
+
+
 def _paged_packed(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_groups: int) -> torch.Tensor:
     """``[1, heads, total_queries, dim]`` in, the same out; the kernel works token-first."""
     from liteinfer_amd.paged_kernels import paged_prefill
 
     # The host lengths, when the payload carries them, say whether the pass
-    # has one-query sequences for the decode kernel to take.
-    one_query_rows = (1 in kv.host_query_lens) if kv.host_query_lens else None
+    # has one-query sequences and which kernel should take them.
+    one_query_rows = None
+    if kv.host_query_lens and kv.host_context_lens:
+        one_query_rows = _one_query_rows_to_decode_kernel(
+            kv.host_query_lens, kv.host_context_lens, query.shape[1], kv.key_pool.shape[1], query.shape[-1],
+            kv.key_pool.element_size())
     out = paged_prefill(
         query.squeeze(0).transpose(0, 1), kv.key_pool, kv.value_pool, kv.slot_table, kv.context_lens,
         kv.query_start_loc, kv.max_query_len, scaling, num_kv_groups, one_query_rows=one_query_rows,
