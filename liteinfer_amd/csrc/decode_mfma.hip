@@ -476,7 +476,9 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
 // separate per-head streams (a load-only probe of config 2's rows: +5% for
 // all 8 heads together). A (sequence, group) is split at the same keys for
 // each of its heads; a wave's two partial slots hold the group's HG heads
-// (AttnArgs::part_heads = HG).
+// (AttnArgs::part_heads = HG). Shares are counted in work units (a
+// segment's 32-key tiles plus AttnArgs::seg_cost for starting it), not in
+// keys.
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool F8, int HG>
 __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
@@ -641,9 +643,10 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
 // waves: w_p = 2^(lse_p - max lse), out = sum w_p o_p / sum w_p
 // (paged_kernels.py:574-629, in the log2 domain). One wave per (sequence,
 // head), reading the piece range the wave holding the context's first key
-// recorded; a context no wave boundary cut was written directly. Lane k
-// holds piece k's weight (64 pieces at a time) and the partial rows are read
-// eight pieces at a time so their loads overlap.
+// recorded; a context no wave boundary cut was written directly. Up to
+// eight pieces (the usual case), every piece's LSE and partial row load at
+// once; beyond that, lane k holds piece k's weight (64 pieces at a time) and
+// the partial rows are read eight pieces at a time so their loads overlap.
 template <typename T>
 __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   constexpr int kMaxC = kGenericMaxHeadDim / 64;
