@@ -168,7 +168,31 @@ def _time_rope(batch, tokens, geo, iters=50, num_slots=1 << 20, seed=0):
         torch.cuda.synchronize()
         return statistics.mean(a.elapsed_time(b) for a, b in marks) * 1e3
 
+    def graph_timed(fn, calls=20):
+        """Per-call GPU time of `calls` back-to-back calls captured in one graph (no host launch cost)."""
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(calls):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = max(1, iters // 10)
+        a.record()
+        for _ in range(reps):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / (reps * calls)
+
     fused_us = timed(lambda: rope_kv_write(q, k, v, cos, sin, slots, kp, vp))
+    fused_graph_us = graph_timed(lambda: rope_kv_write(q, k, v, cos, sin, slots, kp, vp))
     unfused_us = timed(unfused)
     n = batch * tokens
     nbytes = n * (2 * 2 * hq * d + 2 * 2 * 2 * hkv * d + 2 * 2 * d + 8)
@@ -178,6 +202,8 @@ def _time_rope(batch, tokens, geo, iters=50, num_slots=1 << 20, seed=0):
         "GB/s": round(nbytes / (fused_us * 1e-6) / 1e9, 1),
         "frac_hbm": round(nbytes / (fused_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "algorithmic_bytes": nbytes,
+        "graph_replay_us": round(fused_graph_us, 2),
+        "graph_replay_frac_hbm": round(nbytes / (fused_graph_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "unfused_torch_ops_us": round(unfused_us, 2),
     }
 
