@@ -265,6 +265,23 @@ def _traffic():
     return None
 
 
+def _only_prefill(workload: str, seed: int, steps: int, warmup: int) -> int:
+    """One packed prefill workload alone: config 3, its 8 chunks, or 8 chunks of 2048 over 8192."""
+    if workload == "c3":
+        step = packed_step("c3", seed=seed)
+    elif workload == "c3_chunks":
+        chunks, _ = c3_shapes(seed)
+        step = packed_step("custom", seed=seed, chunks=chunks, decode_contexts=[])
+    else:
+        step = packed_step("custom", seed=seed, chunks=[(2048, 8192)] * 8, decode_contexts=[])
+    avg = statistics.mean(_time_prefill(step, steps, warmup))
+    flops = prefill_flops(step.host_query_lens, step.host_context_lens, step.geometry)
+    print(json.dumps({"workload": workload, "avg_us": round(avg * 1e3, 2),
+                      "TFLOP/s": round(flops / (avg * 1e-3) / 1e12, 2),
+                      "frac_bf16_peak": round(flops / (avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -277,8 +294,12 @@ def main() -> int:
     parser.add_argument("--copy-calibration", action="store_true",
                         help="first run three 1 GiB device-to-device copies (a reference kernel of known "
                              "size for rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
+    parser.add_argument("--only-prefill", choices=["c3", "c3_chunks", "long"],
+                        help="time only this packed prefill pass (for profiling) and print its line")
     args = parser.parse_args()
 
+    if args.only_prefill and args.gpus == 1:
+        return _only_prefill(args.only_prefill, args.seed, args.steps, args.warmup)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build's paged path has no multi-GPU component "
               "(decode shards by sequence or KV head with no exchange inside attention); run with --gpus 1.",
