@@ -94,3 +94,34 @@ def test_fp8_decode_random_shapes(case):
     out = paged_decode(b.query, kp, vp, b.slot_table, b.context_lens_t, b.scaling, b.groups, k_scale=k_scale,
                        v_scale=v_scale)
     assert_within(out, want, 2e-2, 2e-3)
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_decode_random_long_contexts(case):
+    """Fewer sequences, contexts up to 20,000 keys: many slot chunks per
+    segment, pieces spread over many waves."""
+    rng = np.random.default_rng(7500 + case)
+    num_heads, num_kv_heads = _heads(rng)
+    head_dim = int(rng.choice([64, 128]))
+    batch = int(rng.integers(1, 17))
+    ctx = _contexts(rng, batch, 20000)
+    b = PagedBatch(ctx, dtype=torch.bfloat16, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                   num_slots=65536, seed=7500 + case)
+    out = paged_decode(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.scaling, b.groups)
+    assert_within(out, b.oracle(), 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize("case", range(3))
+def test_prefill_random_long_chunks(case):
+    """Chunks of up to 600 queries over prefixes of up to 4,000 keys, beside one-query rows."""
+    rng = np.random.default_rng(8500 + case)
+    num_heads, num_kv_heads = _heads(rng)
+    batch = int(rng.integers(2, 5))
+    ctx = _contexts(rng, batch, 4600)
+    q = [1 if i % 2 else int(rng.integers(1, min(c, 600) + 1)) for i, c in enumerate(ctx)]
+    b = PagedBatch(ctx, q, dtype=torch.bfloat16, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=128,
+                   num_slots=65536, seed=8500 + case)
+    for one_query_rows in (True, False):
+        out = paged_prefill(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.query_start_loc,
+                            max(q), b.scaling, b.groups, one_query_rows=one_query_rows)
+        assert_within(out, b.oracle(), 2 ** -6, 2e-3)
