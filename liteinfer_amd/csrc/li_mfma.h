@@ -247,4 +247,28 @@ constexpr float kLog2eMfma = 1.4426950408889634f;
 // accumulator.
 constexpr float kLazyRescale = 8.0f;
 
+// acc + the sum of the eight 16-bit weights of an MFMA operand, in fp32:
+// four two-element dot products with (1, 1) (v_dot2_f32_bf16 / _f16).
+template <typename T, typename Frag>
+__device__ __forceinline__ float li_sum_weights(Frag f, float acc) {
+  if constexpr (__is_same(T, li_bf16)) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const b2 x = {f[2 * u], f[2 * u + 1]};
+      acc = __builtin_amdgcn_fdot2_f32_bf16(x, one, acc, false);
+    }
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const h2 x = {f[2 * u], f[2 * u + 1]};
+      acc = __builtin_amdgcn_fdot2(x, one, acc, false);
+    }
+  }
+  return acc;
+}
+
 }  // namespace li

@@ -60,6 +60,10 @@ constexpr int kWaves = 8;
 constexpr int kMinRows = 32 * kWaves;  // rows of a work-group
 constexpr int kStageKeys = 64;
 
+#ifndef LI_PREFILL_PIPE
+#define LI_PREFILL_PIPE 1
+#endif
+
 // Issues this wave's share of the direct-to-LDS loads of the 64 keys whose
 // first key is entry `t` of the staged slots. The stage takes 2 * kInsts
 // instructions each for K and V (kInsts per 32-key half); wave w issues
@@ -444,6 +448,409 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   }  // units
 }
 
+// issue_stage into a layout that keeps the K rows of every stage in one LDS
+// region and the V rows in another (kdst / vdst: this stage's 32-key tiles
+// of K, of V, 32 rows apart), so that the per-lane read addresses of either
+// region plus every buffer's constant offset fit a DS instruction's 16-bit
+// immediate.
+template <typename L, int W>
+__device__ __forceinline__ void issue_stage_split(uint32_t kdst, uint32_t vdst, const char* __restrict__ kpool,
+                                                  const char* __restrict__ vpool, const int* __restrict__ sl,
+                                                  uint32_t row_bytes, int t, int lane, int w) {
+  constexpr int kPer = 2 * L::kInsts / W;
+  static_assert(kPer >= 1 && kPer * W == 2 * L::kInsts, "waves must split the stage's loads evenly");
+  const int rr = lane / L::kCh, nn = lane % L::kCh;
+  uint32_t slot[kPer];
+#pragma unroll
+  for (int ii = 0; ii < kPer; ++ii) {
+    const int p = w * kPer + ii, half = p / L::kInsts, i = p % L::kInsts;
+    slot[ii] = (uint32_t)sl[t + 32 * half + rr * L::kInsts + i];
+  }
+#pragma unroll
+  for (int ii = 0; ii < kPer; ++ii) {
+    const int p = w * kPer + ii, half = p / L::kInsts, i = p % L::kInsts;
+    const int key = rr * L::kInsts + i;
+    const uint32_t off = half * 32 * L::kRowBytes + i * 1024;
+    dma16(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), slot[ii], row_bytes), kdst + off);
+    dma16(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), vdst + off);
+  }
+}
+
+// The 16-bit-pool prefill with the two waves of each SIMD in ping-pong.
+//
+// Same units, rows, LDS tile layout and arithmetic as prefill_mfma; what
+// changes is when a wave does what. A wave's work per 64-key stage j has a
+// matrix phase M(j) -- P V of stage j - 1 and the scores of stage j, 68
+// MFMAs -- and a vector phase V(j) -- mask, row maxima, running-maximum
+// update and the weights of stage j, ~32 exponentials and ~100 other vector
+// instructions per lane. On gfx950 a wave that interleaves its own MFMAs
+// and vector instructions gets the two back to back (measured: 8 MFMAs + 32
+// FMAs in one wave cost the sum of the two), while the matrix core of a
+// SIMD runs at full rate beside another wave's vector work. So waves 0-3
+// and waves 4-7 (the second wave of SIMDs 0-3) run half a stage apart:
+//
+//   half-period   2j          2j + 1
+//   waves 0-3     M(j)        V(j)
+//   waves 4-7     V(j - 1)    M(j)
+//
+// with a work-group barrier between half-periods, so at any time one wave of
+// every SIMD feeds the matrix core while the other runs its softmax. Stage
+// j's K/V tile is read from LDS from half-period 2j (scores, waves 0-3) to
+// 2j + 3 (P V, waves 4-7); LDS holds kPpRing stages, and the direct-to-LDS
+// loads of stage j + kPpRing - 2 go out at half-period 2j, two stages ahead
+// of their first use. Slot indices sit in a ring restaged half at a time, so
+// a unit's key loop never drains.
+constexpr int kPpRing = 4;
+constexpr int kSlotRing = 4096;  // staged slot entries (int32)
+constexpr int kSlotHalfStages = kSlotRing / 2 / kStageKeys;
+
+#ifdef LI_PREFILL_TRACE
+__device__ long long g_pp_trace[8][1024];
+#define LI_TRACE(ev)                                                                              \
+  do {                                                                                            \
+    if (blockIdx.x == 0 && tcount < 1024) {                                                       \
+      const long long t_ = __builtin_amdgcn_s_memtime();                                          \
+      if (lane == 0) g_pp_trace[w][tcount] = (t_ << 4) | (ev);                                    \
+      ++tcount;                                                                                   \
+    }                                                                                             \
+  } while (0)
+#else
+#define LI_TRACE(ev) \
+  do {               \
+  } while (0)
+#endif
+
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp(AttnArgs a) {
+  constexpr int W = 8;
+  using M = Mfma<T>;
+  using Frag = typename M::Frag;
+  using L = TileLayout<D>;
+  constexpr int kSteps = D / 32;
+  constexpr int kBlk = D / 16;  // 16-dim output blocks
+  constexpr int kWaveDma = 2 * (2 * L::kInsts / W);  // loads one wave issues per stage
+  constexpr int kHalf = 32 * L::kRowBytes;  // one 32-key tile's K (or V) rows
+  constexpr int kRegion = 2 * kHalf;          // a stage's K (or V) rows
+  static_assert(kPpRing == 4, "the loop body covers four stages");
+  __shared__ __attribute__((aligned(16))) int sl[kSlotRing];
+  __shared__ __attribute__((aligned(1024))) char kst[kPpRing][kRegion];  // K rows of each stage
+  __shared__ __attribute__((aligned(1024))) char vst[kPpRing][kRegion];  // V rows of each stage
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool late = w >= 4;  // waves 4-7 run half a stage behind
+#ifdef LI_PREFILL_TRACE
+  int tcount = 0;
+#endif
+  const int n = lane & 15, g = lane >> 4;
+
+  const int nqueues = a.num_kv_heads % kPrefillQueues == 0 ? kPrefillQueues : 1;
+  const int qi = blockIdx.x % nqueues;
+  const int heads_per_queue = a.num_kv_heads / nqueues;
+  const int units = a.queue[kPrefillQueues] * heads_per_queue;
+  __shared__ int s_unit;
+  for (;;) {
+  __syncthreads();
+  if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
+  __syncthreads();
+  // Values read from memory are made wave-uniform explicitly, so every
+  // branch on them below is a scalar branch (no exec-masked code paths).
+  const int unit = __builtin_amdgcn_readfirstlane(s_unit);
+  if (unit >= units) break;
+  const int item = __builtin_amdgcn_readfirstlane(a.work[unit / heads_per_queue]);
+  const int seq = item / a.num_qblocks;
+  const int qblock = item % a.num_qblocks;
+  const int kvh = qi + nqueues * (unit % heads_per_queue);
+
+  const int first_tok = __builtin_amdgcn_readfirstlane(a.qsl[seq]);
+  const int nq = __builtin_amdgcn_readfirstlane(a.qsl[seq + 1]) - first_tok;
+  const int bq = a.block_q;
+  const int q0 = qblock * bq;
+  if (q0 >= nq) continue;
+  if (nq == 1 && a.single_query_elsewhere) continue;
+  const int q1 = min(q0 + bq, nq);
+  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx[seq]);
+  const int pos0 = ctx - nq;
+  const int kend = pos0 + q1;
+  const int G = a.groups;
+  const int ns = (kend + kStageKeys - 1) / kStageKeys;  // 64-key stages
+
+  const float sc = a.scale * kLog2eMfma;
+  int pos[2];
+  bool real[2];
+  int tok[2], head[2];
+  Frag qf[2][kSteps];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int row = 32 * w + 16 * nb + n;
+    const int ql = row / G;
+    real[nb] = row < bq * G && q0 + ql < nq;
+    pos[nb] = real[nb] ? pos0 + q0 + ql : kend;
+    tok[nb] = first_tok + q0 + ql;
+    head[nb] = kvh * G + row % G;
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)tok[nb] * a.q_s0 + (int64_t)head[nb] * a.q_s1 + 8 * g;
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      // The softmax scale (times log2 e) is folded into the query, rounded
+      // to T once: scores come out of the matrix cores in log2 units.
+      Frag x = real[nb] ? *reinterpret_cast<const Frag*>(qrow + 32 * j) : Frag{};
+      u32x4_t pw;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>((float)x[2 * u] * sc, (float)x[2 * u + 1] * sc);
+      qf[nb][j] = __builtin_bit_cast(Frag, pw);
+    }
+  }
+  const int lim[2] = {min(pos[0], kend - 1), min(pos[1], kend - 1)};
+  const int lim_lo = min(pos0 + q0, kend - 1);
+  // A wave whose 32 rows are all padding only loads stages and waits at the
+  // barriers.
+  const bool idle = 32 * w >= (q1 - q0) * G;
+
+  const char* kpool = static_cast<const char*>(a.kp) + (int64_t)kvh * a.p_s1 * (int)sizeof(T);
+  const char* vpool = static_cast<const char*>(a.vp) + (int64_t)kvh * a.p_s1 * (int)sizeof(T);
+  const int64_t* srow = a.st + (int64_t)seq * a.st_s;
+  const uint32_t row_bytes = (uint32_t)(a.p_s0 * (int)sizeof(T));
+
+  // Running row maxima m (log2 units; -inf before the first stage) and
+  // -m in the four lanes of an MFMA accumulator: the first MFMA of every
+  // score chain starts from it, so the matrix cores return s - m and the
+  // common stage's weights are exp2 of the scores as they come.
+  float m[2] = {-INFINITY, -INFINITY};
+  floatx4_t cneg[2] = {floatx4_t{0.f, 0.f, 0.f, 0.f}, floatx4_t{0.f, 0.f, 0.f, 0.f}};
+  floatx4_t acc[2][kBlk + 1];  // [kBlk]: the row's sum of weights (MFMA against ones)
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int i = 0; i < kBlk + 1; ++i) acc[nb][i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+  const Frag ones = li_ones<Frag>();
+
+  uint32_t koff[kSteps], voff[kBlk];
+  {
+    const uint32_t kbase = lds_addr(&kst[0][0]), vbase = lds_addr(&vst[0][0]);
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) koff[j] = kbase + L::offset(n, 4 * j + g);
+    const int s16 = lane & 15, a4 = s16 & 3, key = 4 * g + (s16 >> 2);
+#pragma unroll
+    for (int blk = 0; blk < kBlk; ++blk) voff[blk] = vbase + L::voffset(key, 2 * blk + (a4 >> 1)) + 8 * (a4 & 1);
+  }
+
+  // Slot ring: entry k % kSlotRing holds key k's slot (keys past the block's
+  // last one repeat it, so every load reads a real row).
+  auto stage_slots = [&](int k0, int count) {
+    for (int i = tid; i < count; i += 64 * W) sl[(k0 + i) % kSlotRing] = (int)srow[min(k0 + i, kend - 1)];
+  };
+  auto stage_slots_loaders = [&](int k0, int count) {  // waves 0-3
+    for (int i = tid; i < count; i += 256) sl[(k0 + i) % kSlotRing] = (int)srow[min(k0 + i, kend - 1)];
+  };
+  auto issue = [&](int buf, int st) {
+    issue_stage_split<L, W>(lds_addr(kst[buf]), lds_addr(vst[buf]), kpool, vpool, sl, row_bytes,
+                            (st * kStageKeys) % kSlotRing, lane, w);
+  };
+
+  floatx4_t s[2][4];  // scores (log2 units) of the stage between its M and V phases
+  Frag pf[2][2];      // its weights, between its V phase and the next M phase
+
+  // M phase: P V of the stage in buffer PB (when pv), then the scores of the
+  // stage in buffer SB (when qk).
+  // M phase: P V of the stage in buffer PB (when pv), then the scores of the
+  // stage in buffer SB (when qk). LDS reads run four fragments ahead of the
+  // MFMAs that consume them (sched_group_barrier pins the interleave; left
+  // to itself the scheduler issues each read just before its first use and
+  // the wave waits out the LDS latency at every fragment).
+  auto mphase = [&](auto pb_tag, auto sb_tag, bool pv, bool qk) __attribute__((always_inline)) {
+    if (pv) {
+      constexpr uint32_t vb = decltype(pb_tag)::value * kRegion;
+      Frag vf[2][kBlk];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int blk = 0; blk < kBlk; ++blk) {
+          const uint32_t tb = vb + t * kHalf;
+          vf[t][blk] = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + L::kRow16);
+        }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int blk = 0; blk < kBlk; ++blk)
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf[t][blk], pf[nb][t], acc[nb][blk]);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[nb][kBlk] = M::mma(ones, pf[nb][t], acc[nb][kBlk]);
+      // 2 kBlk fragments (two reads each), two MFMAs per fragment.
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int f = 0; f < 2 * kBlk; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        if (f + 4 < 2 * kBlk) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (qk) {
+      constexpr uint32_t kb = decltype(sb_tag)::value * kRegion;
+      Frag kf[4][kSteps];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j) kf[b][j] = lds_read_frag<Frag>(koff[j] + kb + (b >> 1) * kHalf + (b & 1) * L::kRow16);
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j)
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb)
+            s[nb][b] = M::mma(kf[b][j], qf[nb][j], j == 0 ? cneg[nb] : s[nb][b]);
+      // 4 kSteps fragments (one read each), two MFMAs per fragment.
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int f = 0; f < 4 * kSteps; ++f) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        if (f + 4 < 4 * kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // V phase of stage j (first key t0): s holds s - m (log2 units). Mask;
+  // then the lazy running-maximum update: only when some score of a row
+  // beats m by more than kLazyRescale (or on the first stage) does the
+  // stage take the row's maximum across its lanes and move m there by
+  // delta, subtracting delta from the scores and rescaling the accumulator
+  // by exp2(-delta). Most stages move nothing and their weights are exp2 of
+  // the scores as they are, rounded to T.
+  auto vphase = [&](int t0, auto buf_tag) __attribute__((always_inline)) {
+    (void)buf_tag;
+    const bool masked = t0 + kStageKeys - 1 > lim_lo;
+    float lmax[2];
+    bool move = false;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      if (masked) {
+        // Key t0 + 16 b + 4 g + r is visible iff 16 b + r <= lim - t0 - 4 g.
+        const int d = lim[nb] - t0 - 4 * g;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[nb][b][r] = (16 * b + r <= d) ? s[nb][b][r] : -INFINITY;
+      }
+      // A tree of three-input maxima over the lane's 16 scores.
+      const float x0 = fmaxf(fmaxf(s[nb][0][0], s[nb][0][1]), s[nb][0][2]);
+      const float x1 = fmaxf(fmaxf(s[nb][0][3], s[nb][1][0]), s[nb][1][1]);
+      const float x2 = fmaxf(fmaxf(s[nb][1][2], s[nb][1][3]), s[nb][2][0]);
+      const float x3 = fmaxf(fmaxf(s[nb][2][1], s[nb][2][2]), s[nb][2][3]);
+      const float x4 = fmaxf(fmaxf(s[nb][3][0], s[nb][3][1]), s[nb][3][2]);
+      lmax[nb] = fmaxf(fmaxf(fmaxf(x0, x1), x2), fmaxf(fmaxf(x3, x4), s[nb][3][3]));
+      move |= lmax[nb] > kLazyRescale || m[nb] == -INFINITY;
+    }
+    if (__any(move)) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const float mx = li_group_max(lmax[nb]);
+        const bool first = m[nb] == -INFINITY;
+        const float delta = (first || mx > kLazyRescale) ? mx : 0.f;
+        const float alpha = first ? 0.f : __builtin_amdgcn_exp2f(-delta);
+        m[nb] = first ? delta : m[nb] + delta;
+        cneg[nb] = floatx4_t{-m[nb], -m[nb], -m[nb], -m[nb]};
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[nb][b][r] -= delta;
+#pragma unroll
+        for (int kk = 0; kk < kBlk + 1; ++kk)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[nb][kk][r] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        u32x4_t pw;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int b = 2 * t + u / 2, r = 2 * (u % 2);
+          pw[u] = li_pack2<T>(__builtin_amdgcn_exp2f(s[nb][b][r]), __builtin_amdgcn_exp2f(s[nb][b][r + 1]));
+        }
+        pf[nb][t] = __builtin_bit_cast(Frag, pw);
+      }
+  };
+
+  // Stage j (buffer j % kPpRing): the wave's M phase and V phase, each
+  // after a barrier. Waves 4-7 run the same sequence one barrier later, so
+  // their M phase meets the V phase of waves 0-3 and the other way round.
+  // Every wave issues its share of the direct-to-LDS loads in its V phase,
+  // where they delay no matrix work: waves 0-3 load stage j + 2 in V(j)
+  // (half-period 2j + 1), waves 4-7 stage j + 3 in V(j) (half-period
+  // 2j + 2); both land before stage j + 2's first use at half-period
+  // 2j + 4. Each wave waits for its own loads before the barrier that
+  // precedes that first use: waves 0-3 at the top of period j for stage j,
+  // waves 4-7 before their mid barrier of period j for stage j + 1.
+  auto period = [&](auto j_tag, int j) __attribute__((always_inline)) {
+    constexpr int J = decltype(j_tag)::value;
+    using Cur = std::integral_constant<int, J>;
+    using Prev = std::integral_constant<int, (J + kPpRing - 1) % kPpRing>;
+    LI_TRACE(0);
+    if (!late) li_wait_vm<kWaveDma>();
+    __syncthreads();
+    LI_TRACE(1);
+    if (!idle) mphase(Prev{}, Cur{}, j > 0, j < ns);
+    LI_TRACE(2);
+    if (late) li_wait_vm<kWaveDma>();
+    __syncthreads();
+    LI_TRACE(3);
+    if (j < ns) {
+      const int st = j + (late ? 3 : 2);
+      if (!late && st % kSlotHalfStages == 0 && st + kSlotHalfStages < ns)
+        stage_slots_loaders((st + kSlotHalfStages) * kStageKeys, kSlotRing / 2);
+      issue((J + (late ? 3 : 2)) % kPpRing, min(st, ns - 1));
+      LI_TRACE(4);
+      if (!idle) vphase(j * kStageKeys, Cur{});
+    }
+  };
+
+  // Prologue: slots; stages 0 and 1 in flight, and waves 4-7's share of
+  // stage 2.
+  __syncthreads();  // the previous unit's waves are done with the slot ring
+  stage_slots(0, kSlotRing);
+  __syncthreads();
+  issue(0, 0);
+  issue(1, min(1, ns - 1));
+  if (late) {
+    issue(2, min(2, ns - 1));
+    li_wait_vm<2 * kWaveDma>();  // stage 0
+    __syncthreads();             // waves 4-7 start one barrier late
+  }
+  for (int j = 0; j <= ns; j += kPpRing) {
+    period(std::integral_constant<int, 0>{}, j);
+    if (j + 1 > ns) break;
+    period(std::integral_constant<int, 1>{}, j + 1);
+    if (j + 2 > ns) break;
+    period(std::integral_constant<int, 2>{}, j + 2);
+    if (j + 3 > ns) break;
+    period(std::integral_constant<int, 3>{}, j + 3);
+  }
+  if (!late) __syncthreads();  // the barrier waves 4-7 took first
+  li_wait_vm<0>();
+
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const float lt = acc[nb][kBlk][0];
+    if (!real[nb]) continue;
+    const float inv = 1.f / lt;
+    T* orow = static_cast<T*>(a.out) + (int64_t)tok[nb] * a.o_s0 + (int64_t)head[nb] * a.o_s1 + 4 * g;
+#pragma unroll
+    for (int blk = 0; blk < kBlk; ++blk) {
+      uint2 wv;
+      wv.x = li_pack2<T>(acc[nb][blk][0] * inv, acc[nb][blk][1] * inv);
+      wv.y = li_pack2<T>(acc[nb][blk][2] * inv, acc[nb][blk][3] * inv);
+      *reinterpret_cast<uint2*>(orow + 16 * blk) = wv;
+    }
+  }
+  }  // units
+}
+
 // Work list of the prefill grid: every non-empty query block
 // (sequence * num_qblocks + block), a sequence's blocks side by side, last
 // (heaviest) block first, the sequences ordered by the 32-key tiles of their
@@ -566,6 +973,14 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
   if (a.kv_fp8) {
     if (dtype == LI_BF16) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true>), g, block, 0, s, a);
     else hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true>), g, block, 0, s, a);
+  } else if (LI_PREFILL_PIPE) {
+    if (dtype == LI_BF16) {
+      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_bf16, 128>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((prefill_pp<li_bf16, 64>), g, block, 0, s, a);
+    } else {
+      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_f16, 128>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((prefill_pp<li_f16, 64>), g, block, 0, s, a);
+    }
   } else if (dtype == LI_BF16) {
     if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, false>), g, block, 0, s, a);
     else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64, W, false>), g, block, 0, s, a);
@@ -577,5 +992,11 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
 }
 
 int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) { return launch_prefill_waves<kWaves>(in, dtype, s); }
+
+#ifdef LI_PREFILL_TRACE
+extern "C" int li_prefill_trace(long long* host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pp_trace), sizeof(g_pp_trace));
+}
+#endif
 
 }  // namespace li
