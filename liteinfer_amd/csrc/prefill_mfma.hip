@@ -549,11 +549,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int qi = blockIdx.x % nqueues;
   const int heads_per_queue = a.num_kv_heads / nqueues;
   const int units = a.queue[kPrefillQueues] * heads_per_queue;
+  // Work-group barriers here order LDS only (lds_barrier): a unit's output
+  // stores and the loads in flight never hold a barrier up.
   __shared__ int s_unit;
-  for (;;) {
-  __syncthreads();
   if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
-  __syncthreads();
+  int next_unit = 0;  // tid 0: the unit claimed for after this one
+  for (;;) {
+  lds_barrier();
+  LI_TRACE(5);
   // Values read from memory are made wave-uniform explicitly, so every
   // branch on them below is a scalar branch (no exec-masked code paths).
   const int unit = __builtin_amdgcn_readfirstlane(s_unit);
@@ -575,6 +578,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int kend = pos0 + q1;
   const int G = a.groups;
   const int ns = (kend + kStageKeys - 1) / kStageKeys;  // 64-key stages
+  // The next unit is claimed a few stages before this one ends, so the
+  // atomic's round trip is hidden, yet late enough that a work-group that
+  // finishes early still takes the heaviest unit left.
+  const int claim_at = max(ns - 3, 0);
 
   const float sc = a.scale * kLog2eMfma;
   int pos[2];
@@ -655,63 +662,74 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // stage in buffer SB (when qk).
   // M phase: P V of the stage in buffer PB (when pv), then the scores of the
   // stage in buffer SB (when qk). LDS reads run four fragments ahead of the
-  // MFMAs that consume them (sched_group_barrier pins the interleave; left
-  // to itself the scheduler issues each read just before its first use and
-  // the wave waits out the LDS latency at every fragment).
-  auto mphase = [&](auto pb_tag, auto sb_tag, bool pv, bool qk) __attribute__((always_inline)) {
-    if (pv) {
-      constexpr uint32_t vb = decltype(pb_tag)::value * kRegion;
-      Frag vf[2][kBlk];
+  // MFMAs that consume them, across the boundary between the two parts
+  // (sched_group_barrier pins the interleave; left to itself the scheduler
+  // issues each read just before its first use and the wave waits out the
+  // LDS latency at every fragment).
+  constexpr int kVFrags = 2 * kBlk;    // V^T fragments of a stage (two reads each)
+  constexpr int kKFrags = 4 * kSteps;  // K fragments of a stage (one read each)
+  auto read_v = [&](uint32_t vb, Frag (&vf)[2][kBlk]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int blk = 0; blk < kBlk; ++blk) {
-          const uint32_t tb = vb + t * kHalf;
-          vf[t][blk] = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + L::kRow16);
-        }
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int blk = 0; blk < kBlk; ++blk)
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf[t][blk], pf[nb][t], acc[nb][blk]);
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[nb][kBlk] = M::mma(ones, pf[nb][t], acc[nb][kBlk]);
-      // 2 kBlk fragments (two reads each), two MFMAs per fragment.
-      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
-#pragma unroll
-      for (int f = 0; f < 2 * kBlk; ++f) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        if (f + 4 < 2 * kBlk) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      for (int blk = 0; blk < kBlk; ++blk) {
+        const uint32_t tb = vb + t * kHalf;
+        vf[t][blk] = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + L::kRow16);
       }
-      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-      __builtin_amdgcn_sched_barrier(0);
+  };
+  auto read_k = [&](uint32_t kb, Frag (&kf)[4][kSteps]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < kSteps; ++j) kf[b][j] = lds_read_frag<Frag>(koff[j] + kb + (b >> 1) * kHalf + (b & 1) * L::kRow16);
+  };
+  auto pv_mfma = [&](const Frag (&vf)[2][kBlk]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int blk = 0; blk < kBlk; ++blk)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[nb][blk] = M::mma(vf[t][blk], pf[nb][t], acc[nb][blk]);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acc[nb][kBlk] = M::mma(ones, pf[nb][t], acc[nb][kBlk]);
+  };
+  auto qk_mfma = [&](const Frag (&kf)[4][kSteps]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int j = 0; j < kSteps; ++j)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) s[nb][b] = M::mma(kf[b][j], qf[nb][j], j == 0 ? cneg[nb] : s[nb][b]);
+  };
+  // Every period runs the same M phase: at j = 0 its P V reads a zeroed
+  // buffer with zero weights (a no-op), and at j = ns its scores go unused.
+  auto mphase = [&](auto pb_tag, auto sb_tag) __attribute__((always_inline)) {
+    constexpr uint32_t vb = decltype(pb_tag)::value * kRegion;
+    constexpr uint32_t kb = decltype(sb_tag)::value * kRegion;
+    Frag vf[2][kBlk];
+    Frag kf[4][kSteps];
+    read_v(vb, vf);
+    pv_mfma(vf);
+    read_k(kb, kf);
+    qk_mfma(kf);
+    // Reads of fragment f + 4 go out with the MFMAs of fragment f; the
+    // first K fragments with the last V^T fragments' MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+    for (int f = 0; f < kVFrags; ++f) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      if (f + 4 < kVFrags) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
-    if (qk) {
-      constexpr uint32_t kb = decltype(sb_tag)::value * kRegion;
-      Frag kf[4][kSteps];
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // row sums
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int j = 0; j < kSteps; ++j) kf[b][j] = lds_read_frag<Frag>(koff[j] + kb + (b >> 1) * kHalf + (b & 1) * L::kRow16);
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-#pragma unroll
-        for (int j = 0; j < kSteps; ++j)
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb)
-            s[nb][b] = M::mma(kf[b][j], qf[nb][j], j == 0 ? cneg[nb] : s[nb][b]);
-      // 4 kSteps fragments (one read each), two MFMAs per fragment.
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-      for (int f = 0; f < 4 * kSteps; ++f) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-        if (f + 4 < 4 * kSteps) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int f = 0; f < kKFrags; ++f) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      if (f + 4 < kKFrags) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
   // V phase of stage j (first key t0): s holds s - m (log2 units). Mask;
   // then the lazy running-maximum update: only when some score of a row
@@ -792,47 +810,81 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     using Cur = std::integral_constant<int, J>;
     using Prev = std::integral_constant<int, (J + kPpRing - 1) % kPpRing>;
     LI_TRACE(0);
-    if (!late) li_wait_vm<kWaveDma>();
-    __syncthreads();
+    // Only stages that exist are loaded, so near the end fewer loads are
+    // newer than the one waited for.
+    if (!late) {
+      if (j + 1 < ns) li_wait_vm<kWaveDma>();
+      else li_wait_vm<0>();
+    }
+    lds_barrier();
     LI_TRACE(1);
-    if (!idle) mphase(Prev{}, Cur{}, j > 0, j < ns);
+    if (j == claim_at && tid == 0) next_unit = claim_async(&a.queue[qi]);
+    if (!idle) mphase(Prev{}, Cur{});
     LI_TRACE(2);
-    if (late) li_wait_vm<kWaveDma>();
-    __syncthreads();
+    if (late) {
+      if (j + 2 < ns) li_wait_vm<kWaveDma>();
+      else li_wait_vm<0>();
+    }
+    lds_barrier();
     LI_TRACE(3);
     if (j < ns) {
       const int st = j + (late ? 3 : 2);
       if (!late && st % kSlotHalfStages == 0 && st + kSlotHalfStages < ns)
         stage_slots_loaders((st + kSlotHalfStages) * kStageKeys, kSlotRing / 2);
-      issue((J + (late ? 3 : 2)) % kPpRing, min(st, ns - 1));
+      if (st < ns) issue((J + (late ? 3 : 2)) % kPpRing, st);
       LI_TRACE(4);
       if (!idle) vphase(j * kStageKeys, Cur{});
     }
   };
 
-  // Prologue: slots; stages 0 and 1 in flight, and waves 4-7's share of
-  // stage 2.
-  __syncthreads();  // the previous unit's waves are done with the slot ring
-  stage_slots(0, kSlotRing);
-  __syncthreads();
+  LI_TRACE(6);
+  // Prologue: slots; the V rows of the last buffer zeroed (the first M
+  // phase's P V reads them, with zero weights); stages 0 and 1 in flight,
+  // and waves 4-7's share of stage 2.
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) pf[nb][t] = Frag{};
+  stage_slots(0, min(kSlotRing, ns * kStageKeys));
+  for (int i = tid; i < kRegion / 16; i += 64 * W)
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(
+        (uintptr_t)(lds_addr(vst[kPpRing - 1]) + 16 * i)) = u32x4_t{0u, 0u, 0u, 0u};
+  lds_barrier();
   issue(0, 0);
-  issue(1, min(1, ns - 1));
+  if (ns > 1) issue(1, 1);
   if (late) {
-    issue(2, min(2, ns - 1));
-    li_wait_vm<2 * kWaveDma>();  // stage 0
-    __syncthreads();             // waves 4-7 start one barrier late
+    if (ns > 2) {
+      issue(2, 2);
+      li_wait_vm<2 * kWaveDma>();  // stage 0
+    } else if (ns > 1) {
+      li_wait_vm<kWaveDma>();
+    } else {
+      li_wait_vm<0>();
+    }
+    lds_barrier();               // waves 4-7 start one barrier late
   }
-  for (int j = 0; j <= ns; j += kPpRing) {
+  for (int j = 0; j < ns; j += kPpRing) {
     period(std::integral_constant<int, 0>{}, j);
-    if (j + 1 > ns) break;
+    if (j + 1 >= ns) break;
     period(std::integral_constant<int, 1>{}, j + 1);
-    if (j + 2 > ns) break;
+    if (j + 2 >= ns) break;
     period(std::integral_constant<int, 2>{}, j + 2);
-    if (j + 3 > ns) break;
+    if (j + 3 >= ns) break;
     period(std::integral_constant<int, 3>{}, j + 3);
   }
-  if (!late) __syncthreads();  // the barrier waves 4-7 took first
+  // The last period: P V of the last stage only (every load has landed).
   li_wait_vm<0>();
+  lds_barrier();
+  if (!idle) {
+    Frag vf[2][kBlk];
+    read_v(lds_addr(vst[(ns - 1) % kPpRing]) - lds_addr(vst[0]), vf);
+    pv_mfma(vf);
+  }
+  lds_barrier();
+  if (!late) lds_barrier();  // the barrier waves 4-7 took first
+  if (tid == 0) s_unit = next_unit;
+  LI_TRACE(8);
+  LI_TRACE(7);
 
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
@@ -848,6 +900,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       *reinterpret_cast<uint2*>(orow + 16 * blk) = wv;
     }
   }
+  LI_TRACE(9);
   }  // units
 }
 
