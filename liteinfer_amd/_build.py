@@ -40,6 +40,15 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-source extra flags. prefill_mfma.hip: its persistent kernel claims the
+# next unit with an atomic whose old value it reads only at the unit's end;
+# the wave-level atomic optimizer would read it back at once, stalling the
+# wave on every load in flight.
+SOURCE_FLAGS = {
+    "prefill_mfma.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     path = Path(rocm) / "bin" / "hipcc"
@@ -56,7 +65,7 @@ def sources() -> list[Path]:
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *DEVICE_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so; that
     # warning is harmless and is the only output dropped.

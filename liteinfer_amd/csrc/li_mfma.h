@@ -155,16 +155,6 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
 }
 
-// atomicAdd(counter, 1) whose result is read only after a later wait for
-// all of this wave's vector-memory operations (li_wait_vm<0>): written as
-// inline assembly because the compiler would wait for the old value (and
-// with it for every load in flight) right after issuing the atomic.
-__device__ __forceinline__ int claim_async(int* counter) {
-  int old;
-  asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(old) : "v"(counter), "v"(1) : "memory");
-  return old;
-}
-
 // Waits until at most N vector-memory operations of this wave are in flight.
 template <int N>
 __device__ __forceinline__ void li_wait_vm() {

@@ -506,6 +506,12 @@ constexpr int kSlotHalfStages = kSlotRing / 2 / kStageKeys;
 
 #ifdef LI_PREFILL_TRACE
 __device__ long long g_pp_trace[8][1024];
+__device__ long long g_pp_units[256][64];  // per work-group: (time << 20 | ns << 1 | end) per unit event
+#define LI_UNIT_TRACE(endflag, nsv)                                                              \
+  do {                                                                                            \
+    if (tid == 0 && blockIdx.x < 256 && ucount < 64)                                              \
+      g_pp_units[blockIdx.x][ucount++] = (__builtin_amdgcn_s_memtime() << 20) | ((nsv) << 1) | (endflag); \
+  } while (0)
 #define LI_TRACE(ev)                                                                              \
   do {                                                                                            \
     if (blockIdx.x == 0 && tcount < 1024) {                                                       \
@@ -517,6 +523,9 @@ __device__ long long g_pp_trace[8][1024];
 #else
 #define LI_TRACE(ev) \
   do {               \
+  } while (0)
+#define LI_UNIT_TRACE(endflag, nsv) \
+  do {                              \
   } while (0)
 #endif
 
@@ -541,7 +550,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool late = w >= 4;  // waves 4-7 run half a stage behind
 #ifdef LI_PREFILL_TRACE
-  int tcount = 0;
+  int tcount = 0, ucount = 0;
 #endif
   const int n = lane & 15, g = lane >> 4;
 
@@ -582,6 +591,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // atomic's round trip is hidden, yet late enough that a work-group that
   // finishes early still takes the heaviest unit left.
   const int claim_at = max(ns - 3, 0);
+  LI_UNIT_TRACE(0, ns);
 
   const float sc = a.scale * kLog2eMfma;
   int pos[2];
@@ -818,7 +828,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     lds_barrier();
     LI_TRACE(1);
-    if (j == claim_at && tid == 0) next_unit = claim_async(&a.queue[qi]);
+    // The old value is first read after the unit's last wait for every
+    // load, where the compiler places its wait for the atomic (this file is
+    // built with the wave-level atomic optimizer off, which would otherwise
+    // read the value back at once and wait for every load in flight).
+    if (j == claim_at && tid == 0) next_unit = atomicAdd(&a.queue[qi], 1);
     if (!idle) mphase(Prev{}, Cur{});
     LI_TRACE(2);
     if (late) {
@@ -884,6 +898,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (!late) lds_barrier();  // the barrier waves 4-7 took first
   if (tid == 0) s_unit = next_unit;
   LI_TRACE(8);
+  LI_UNIT_TRACE(1, ns);
   LI_TRACE(7);
 
 #pragma unroll
@@ -1049,6 +1064,13 @@ int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) { return l
 #ifdef LI_PREFILL_TRACE
 extern "C" int li_prefill_trace(long long* host) {
   return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pp_trace), sizeof(g_pp_trace));
+}
+extern "C" int li_prefill_unit_trace(long long* host) {
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pp_units), sizeof(g_pp_units));
+}
+extern "C" int li_prefill_unit_trace_clear() {
+  static long long zero[256][64];
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_pp_units), zero, sizeof(zero));
 }
 #endif
 
