@@ -504,6 +504,21 @@ constexpr int kPpRing = 4;
 constexpr int kSlotRing = 4096;  // staged slot entries (int32)
 constexpr int kSlotHalfStages = kSlotRing / 2 / kStageKeys;
 
+#ifndef LI_PP_SETPRIO
+#define LI_PP_SETPRIO 1
+#endif
+#if LI_PP_SETPRIO
+#define LI_SETPRIO_HI() __builtin_amdgcn_s_setprio(2)
+#define LI_SETPRIO_LO() __builtin_amdgcn_s_setprio(0)
+#else
+#define LI_SETPRIO_HI() \
+  do {                  \
+  } while (0)
+#define LI_SETPRIO_LO() \
+  do {                  \
+  } while (0)
+#endif
+
 #ifdef LI_PREFILL_TRACE
 __device__ long long g_pp_trace[8][1024];
 __device__ long long g_pp_units[256][64];  // per work-group: (time << 20 | ns << 1 | end) per unit event
@@ -833,7 +848,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // built with the wave-level atomic optimizer off, which would otherwise
     // read the value back at once and wait for every load in flight).
     if (j == claim_at && tid == 0) next_unit = atomicAdd(&a.queue[qi], 1);
-    if (!idle) mphase(Prev{}, Cur{});
+    if (!idle) {
+      // The matrix phase issues ahead of the other wave's vector work on
+      // its SIMD: an MFMA that waits for issue leaves the matrix core idle.
+      LI_SETPRIO_HI();
+      mphase(Prev{}, Cur{});
+      LI_SETPRIO_LO();
+    }
     LI_TRACE(2);
     if (late) {
       if (j + 2 < ns) li_wait_vm<kWaveDma>();
