@@ -175,6 +175,8 @@ int li_choose_num_splits(int batch, int num_kv_heads, int max_context,
  * under any schedule it may run (the MFMA kernel's balanced split included).
  * num_splits = 0 chooses (fixed-length partitions, so a long context is cut
  * more finely than a short one); num_splits >= 1 is the equal-slice split.
+ * num_cus shapes the partition policy only: the workspace is always sized for
+ * the current device, whose CU count sizes the MFMA kernel's balanced grid.
  */
 int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads,
                          int head_dim, int max_context, int num_splits,
@@ -230,7 +232,9 @@ int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q_stride_hea
  * the decode kernel serves with a partitioned key axis, and the list that
  * orders the prefill kernel's query blocks longest first. No counterpart in
  * the reference, whose prefill kernel allocates nothing
- * (liteinfer/models/paged_kernels.py:867).
+ * (liteinfer/models/paged_kernels.py:867). The size is for the current
+ * device (its CU count sizes the grid the launch runs); num_cus is accepted
+ * for symmetry with li_paged_decode_plan and does not change it.
  */
 int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
                           int head_dim, int max_context, int num_cus,

@@ -47,6 +47,19 @@ __global__ __launch_bounds__(64) void attend_generic(AttnArgs a) {
   const int q0 = qblock * a.block_q;
   if (q0 >= nq) return;
   const int q1 = min(q0 + a.block_q, nq);
+  if (ctx <= 0) {
+    // A decode row with no key to attend to: the reference's softmax over
+    // nothing is 0 / 0.
+    if (part == 0) {
+      for (int qi = q0; qi < q1; ++qi)
+        for (int h = 0; h < a.groups; ++h) {
+          T* orow = static_cast<T*>(a.out) + (int64_t)(first_tok + qi) * a.o_s0 +
+                    (int64_t)(kvh * a.groups + h) * a.o_s1;
+          for (int d = threadIdx.x; d < a.head_dim; d += blockDim.x) orow[d] = li_quiet_nan<T>();
+        }
+    }
+    return;
+  }
 
   int kb = 0, ke = ctx, nparts = 1;
   if (a.part_o) {

@@ -326,6 +326,15 @@ __global__ __launch_bounds__(64) void decode_partitioned(AttnArgs a) {
   const int row = decode_row(a, seq);
   if (row < 0) return;
   const int ctx = a.ctx[seq];
+  if (ctx <= 0) {
+    // No key to attend to: the reference's softmax over nothing is 0 / 0.
+    if (part == 0) {
+      T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)kvh * a.groups * a.o_s1;
+      for (int h = 0; h < a.groups; ++h)
+        for (int d = threadIdx.x; d < D; d += 64) orow[(int64_t)h * a.o_s1 + d] = li_quiet_nan<T>();
+    }
+    return;
+  }
   const int plen = a.part_len > 0 ? a.part_len : max(1, (ctx + a.num_parts - 1) / a.num_parts);
   const int kb = part * plen;
   if (kb >= ctx) return;
@@ -660,7 +669,18 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   // issued before either is used.
   const int keys = decode_keys(a, seq);
   const int4 info = a.pieces[(int64_t)seq * a.num_kv_heads + kvh];
-  if (keys == 0) return;
+  if (keys == 0) {
+    // A decode row with no key to attend to: the reference's softmax over
+    // nothing is 0 / 0. (In a packed pass every sequence that is not a
+    // one-query row also counts 0 keys here, and has no row: decode_row is
+    // -1 and nothing is written.)
+    const int zrow = decode_row(a, seq);
+    if (zrow >= 0) {
+      T* orow = static_cast<T*>(a.out) + (int64_t)zrow * a.o_s0 + (int64_t)head * a.o_s1;
+      for (int d = lane; d < D; d += 64) orow[d] = li_quiet_nan<T>();
+    }
+    return;
+  }
   const int w0 = info.x, w1 = info.y, slot0 = info.z;
   if (w1 <= w0) return;
   const int n = w1 - w0 + 1;

@@ -46,8 +46,8 @@ __device__ __forceinline__ float to_f32(E x) {
 // Two values to e4m3 in the low (HIGH = false) or high 16 bits of `into`.
 template <bool HIGH>
 __device__ __forceinline__ uint32_t pack_fp8(float a, float b, uint32_t into) {
-  a = fminf(fmaxf(a, -448.f), 448.f);
-  b = fminf(fmaxf(b, -448.f), 448.f);
+  a = li_clamp_e4m3(a);
+  b = li_clamp_e4m3(b);
   return __builtin_amdgcn_cvt_pk_fp8_f32(a, b, into, HIGH);
 }
 

@@ -68,6 +68,23 @@ __device__ __forceinline__ li_bf16 li_from_float<li_bf16>(float x) { return (li_
 template <>
 __device__ __forceinline__ li_f16 li_from_float<li_f16>(float x) { return (li_f16)x; }
 
+// A quiet NaN of T, from its bit pattern (the sources build with
+// -fno-honor-nans, under which a NaN constant is not guaranteed).
+template <typename T>
+__device__ __forceinline__ T li_quiet_nan() {
+  if constexpr (sizeof(T) == 4) return __builtin_bit_cast(T, 0x7fc00000u);
+  else if constexpr (__is_same(T, li_bf16)) return __builtin_bit_cast(T, (unsigned short)0x7fc0u);
+  else return __builtin_bit_cast(T, (unsigned short)0x7e00u);
+}
+
+// x clamped to the e4m3 range [-448, 448], a NaN passed through (tested on
+// the bits: the sources build with -fno-honor-nans, under which x != x may
+// fold to false), so it stores as the e4m3 NaN as torch's cast does.
+__device__ __forceinline__ float li_clamp_e4m3(float x) {
+  if ((__float_as_uint(x) & 0x7fffffffu) > 0x7f800000u) return x;
+  return fminf(fmaxf(x, -448.f), 448.f);
+}
+
 // Bit pattern of two 16-bit elements packed low-first, from fp32 values
 // rounded to nearest even.
 template <typename T>

@@ -175,9 +175,10 @@ extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, 
   if (partition_len) *partition_len = plen;
   size_t need = decode_workspace(batch, num_heads, head_dim, parts);
   // The MFMA kernel runs the balanced split unless LI_FLAG_EQUAL_SPLITS pins
-  // the partitions; size for either.
-  if (num_cus <= 0) num_cus = device_cu_count();
-  need = std::max(need, balanced_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch, num_kv_heads));
+  // the partitions; size for either. The balanced grid is sized from the
+  // current device's CU count whatever num_cus says, as the launch sizes it.
+  need = std::max(need, balanced_workspace(balanced_waves(device_cu_count()), num_heads / num_kv_heads, head_dim,
+                                           batch, num_kv_heads));
   if (workspace_bytes) *workspace_bytes = need;
   return LI_OK;
 }
@@ -316,9 +317,11 @@ extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
   clear_error();
   if (int rc = check_common(LI_BF16, num_heads, num_kv_heads, head_dim, "li_paged_prefill_plan")) return rc;
   if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_prefill_plan: negative extent");
-  if (num_cus <= 0) num_cus = device_cu_count();
+  // Sized for the current device's CU count (the launch's), whatever
+  // num_cus says.
+  (void)num_cus;
   if (workspace_bytes)
-    *workspace_bytes = prefill_workspace(balanced_waves(num_cus), num_heads / num_kv_heads, head_dim, batch,
+    *workspace_bytes = prefill_workspace(balanced_waves(device_cu_count()), num_heads / num_kv_heads, head_dim, batch,
                                          num_kv_heads, max_context);
   return LI_OK;
 }

@@ -504,11 +504,14 @@ constexpr int kPpRing = 4;
 constexpr int kSlotRing = 4096;  // staged slot entries (int32)
 constexpr int kSlotHalfStages = kSlotRing / 2 / kStageKeys;
 
+#ifndef LI_PP_PRIO_M
+#define LI_PP_PRIO_M 2
+#endif
 #ifndef LI_PP_SETPRIO
 #define LI_PP_SETPRIO 1
 #endif
 #if LI_PP_SETPRIO
-#define LI_SETPRIO_HI() __builtin_amdgcn_s_setprio(2)
+#define LI_SETPRIO_HI() __builtin_amdgcn_s_setprio(LI_PP_PRIO_M)
 #define LI_SETPRIO_LO() __builtin_amdgcn_s_setprio(0)
 #else
 #define LI_SETPRIO_HI() \

@@ -57,7 +57,7 @@ template <typename VecE>
 __device__ __forceinline__ uint2 quant8(VecE x, float inv) {
   float f[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(li_to_float(x[e]) * inv, -448.f), 448.f);
+  for (int e = 0; e < 8; ++e) f[e] = li_clamp_e4m3(li_to_float(x[e]) * inv);
   uint2 out;
   out.x = __builtin_amdgcn_cvt_pk_fp8_f32(f[0], f[1], 0u, false);
   out.x = __builtin_amdgcn_cvt_pk_fp8_f32(f[2], f[3], out.x, true);

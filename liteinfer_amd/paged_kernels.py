@@ -213,6 +213,31 @@ def kv_scatter(
     _native.check(status, "kv_scatter")
 
 
+def _decode_inputs(query, key_pool, value_pool, slot_table, context_lens, num_kv_groups, num_splits,
+                   k_scale, v_scale):
+    """paged_decode's argument checks (the reference's messages) and the layouts its kernels take."""
+    if key_pool.stride() != value_pool.stride():
+        raise ValueError("key and value pools must be laid out identically")
+    if num_splits is not None and num_splits < 1:
+        raise ValueError(f"num_splits must be >= 1, got {num_splits}")
+    device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens)
+    _check_pools(key_pool, value_pool)
+    _, num_heads, head_dim = query.shape
+    kv_code = _kv_dtype_code(query, key_pool, k_scale, v_scale)
+    if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:
+        raise ValueError(
+            f"{num_heads} query heads in groups of {num_kv_groups} do not match {key_pool.shape[1]} KV heads"
+        )
+    if head_dim != key_pool.shape[2]:
+        raise ValueError(f"query head_dim {head_dim} does not match the pool's {key_pool.shape[2]}")
+    query = _last_dim_contiguous(query)
+    slot_table = _as_index(slot_table, torch.int64)
+    if slot_table.stride(-1) != 1:
+        slot_table = slot_table.contiguous()
+    context_lens = _as_index(context_lens, torch.int32).contiguous()
+    return device, query, slot_table, context_lens, kv_code
+
+
 def paged_decode(
     query: torch.Tensor,
     key_pool: torch.Tensor,
@@ -259,25 +284,9 @@ def paged_decode(
     Returns:
         ``[batch, num_heads, head_dim]``, same dtype as ``query``.
     """
-    if key_pool.stride() != value_pool.stride():
-        raise ValueError("key and value pools must be laid out identically")
-    if num_splits is not None and num_splits < 1:
-        raise ValueError(f"num_splits must be >= 1, got {num_splits}")
-    device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens)
-    _check_pools(key_pool, value_pool)
+    device, query, slot_table, context_lens, kv_code = _decode_inputs(
+        query, key_pool, value_pool, slot_table, context_lens, num_kv_groups, num_splits, k_scale, v_scale)
     batch, num_heads, head_dim = query.shape
-    kv_code = _kv_dtype_code(query, key_pool, k_scale, v_scale)
-    if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:
-        raise ValueError(
-            f"{num_heads} query heads in groups of {num_kv_groups} do not match {key_pool.shape[1]} KV heads"
-        )
-    if head_dim != key_pool.shape[2]:
-        raise ValueError(f"query head_dim {head_dim} does not match the pool's {key_pool.shape[2]}")
-    query = _last_dim_contiguous(query)
-    slot_table = _as_index(slot_table, torch.int64)
-    if slot_table.stride(-1) != 1:
-        slot_table = slot_table.contiguous()
-    context_lens = _as_index(context_lens, torch.int32).contiguous()
     num_kv_heads = key_pool.shape[1]
     max_context = slot_table.shape[1]
 
@@ -324,6 +333,7 @@ def paged_prefill(
     one_query_rows: bool | None = None,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attend each sequence's chunk of queries over the KV its slots address, causally.
 
@@ -350,9 +360,12 @@ def paged_prefill(
             ``False`` lets the prefill kernel serve every sequence and skips
             the decode launch. Either way the result is the same attention.
         k_scale, v_scale: the scales of an fp8 pool (see `paged_decode`).
+        out: where to write the result (the query's shape and dtype, last
+            axis contiguous, any other strides); a new tensor when None.
 
     Returns:
-        ``[total_queries, num_heads, head_dim]`` with the strides of `query`.
+        ``[total_queries, num_heads, head_dim]`` (`out`, or a new tensor with
+        the strides of `query`).
     """
     if key_pool.stride() != value_pool.stride():
         raise ValueError("key and value pools must be laid out identically")
@@ -385,7 +398,11 @@ def paged_prefill(
         _native.ctypes.byref(need),
     )
     _native.check(status, "paged_prefill")
-    out = torch.empty_like(query)
+    if out is None:
+        out = torch.empty_like(query)
+    elif (out.shape != query.shape or out.dtype != query.dtype or out.device != query.device
+          or out.stride(-1) != 1):
+        raise ValueError("out must match the query's shape, dtype and device, with a contiguous last axis")
     workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
     status = lib.li_paged_prefill_ex(
         query.data_ptr(), query.stride(0), query.stride(1),

@@ -53,6 +53,11 @@ def attend(
         if nq == 0:
             continue
         ctx = int(context_lens[i])
+        if ctx <= 0:
+            # Nothing to attend to: the reference's softmax over all-masked
+            # scores is 0 / 0 (liteinfer/models/attention.py:158-164).
+            out[first:first + nq] = np.nan
+            continue
         slots = np.asarray(slot_table[i, :ctx], dtype=np.int64)
         keys = key_pool[slots].astype(dtype)      # [ctx, Hkv, D]
         values = value_pool[slots].astype(dtype)

@@ -81,10 +81,20 @@ def encode(x: np.ndarray) -> np.ndarray:
 
 
 def quantize(x: np.ndarray, scale: float) -> np.ndarray:
-    """Pool codes of x (any float array) for a positive scale, as the slot-write stores them."""
+    """Pool codes of x (any float array) for a positive scale, as the slot-write stores them.
+
+    A NaN stays a NaN (0x7f, or 0xff with its sign bit set), as torch's
+    float8_e4m3fn cast keeps it; everything else is clamped to +-448 first.
+    """
+    x = np.asarray(x, dtype=np.float32)
     inv = np.float32(1.0) / np.float32(scale)
-    y = np.asarray(x, dtype=np.float32) * inv
-    return encode(np.clip(y, -E4M3_MAX, E4M3_MAX))
+    y = x * inv
+    nan = np.isnan(y)
+    codes = encode(np.clip(np.where(nan, 0.0, y), -E4M3_MAX, E4M3_MAX).astype(np.float32))
+    # The sign a NaN keeps is the input's (a product's NaN sign is not fixed
+    # by IEEE 754, so it is taken before the scaling).
+    codes[nan] = np.where(np.signbit(x[nan]), 0xFF, 0x7F).astype(np.uint8)
+    return codes
 
 
 def dequantize(codes: np.ndarray, scale: float) -> np.ndarray:

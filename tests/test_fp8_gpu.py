@@ -239,3 +239,34 @@ def test_fused_rope_write_into_fp8_pools_is_rope_then_quantising_scatter(dtype, 
     kp3 = torch.zeros(num_slots, kvh, d, dtype=dtype, device=DEV)
     q16 = rope_kv_write(q, k, v, cos, sin, slots, kp3, torch.zeros_like(kp3))
     assert torch.equal(q_out, q16) and torch.equal(q_out, want_q)
+
+
+@pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
+def test_quantising_slot_write_passes_nan_through(src_dtype):
+    """A NaN in K or V is stored as the e4m3 NaN (as torch's cast stores it),
+    not clamped to a finite value that would hide the upstream error."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    k = torch.randn(2, 8, 3, 128, generator=g, device=DEV).to(src_dtype)
+    v = torch.randn(2, 8, 3, 128, generator=g, device=DEV).to(src_dtype)
+    k[0, 1, 2, 5] = float("nan")
+    k[1, 7, 0, 127] = -float("nan")
+    v[1, 0, 1, 64] = float("nan")
+    kp = torch.zeros(16, 8, 128, dtype=torch.uint8, device=DEV).view(FP8)
+    vp = torch.zeros_like(kp)
+    slots = torch.tensor([[3, 9, 0, 15, 4, 7]], device=DEV)
+    kv_scatter(kp, vp, slots, k, v)
+    want_k = np.zeros((16, 8, 128), dtype=np.uint8)
+    want_v = np.zeros((16, 8, 128), dtype=np.uint8)
+    kf, vf = to_numpy(k).astype(np.float32), to_numpy(v).astype(np.float32)
+    for i, s in enumerate(slots[0].tolist()):
+        b, t = divmod(i, 3)
+        want_k[s] = fp8.quantize(kf[b, :, t, :], 1.0)
+        want_v[s] = fp8.quantize(vf[b, :, t, :], 1.0)
+    # A NaN's sign is not defined (the hardware's conversion may set it), so
+    # a NaN position must hold one of the two e4m3 NaN codes; every other
+    # code is bit-exact.
+    for got, want in ((_codes(kp), want_k), (_codes(vp), want_v)):
+        nan = (want & 0x7F) == 0x7F
+        assert np.array_equal(got[~nan], want[~nan])
+        assert np.all((got[nan] & 0x7F) == 0x7F)
+    assert nan.sum() == 1 and ((want_k & 0x7F) == 0x7F).sum() == 2

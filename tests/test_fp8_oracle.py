@@ -76,3 +76,13 @@ def test_dequantize_applies_the_scale():
     t = fp8.decode_table()
     ok = np.isfinite(t)
     assert np.array_equal(fp8.dequantize(codes, 0.5)[ok], t[ok] * 0.5)
+
+
+def test_quantize_keeps_a_nan_as_torchs_cast_does():
+    """NaN (either sign) becomes the e4m3 NaN code torch's float8_e4m3fn cast
+    gives it; the clamp applies to numbers only (+-inf saturate to +-448,
+    where torch's unsaturated cast would give NaN)."""
+    x = np.array([np.nan, -np.nan, 3.0, -2.5], dtype=np.float32)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(fp8.quantize(x, 1.0), want)
+    assert np.array_equal(fp8.quantize(np.array([np.inf, -np.inf], dtype=np.float32), 1.0), [0x7E, 0xFE])

@@ -204,3 +204,20 @@ def test_baseline_matches_the_oracle():
                               torch.from_numpy(vp).float(), torch.from_numpy(table), torch.from_numpy(ctx),
                               scale, groups)
         np.testing.assert_allclose(got.numpy(), want, rtol=2e-5, atol=2e-5)
+
+
+def test_a_row_with_no_keys_is_nan():
+    """A decode row whose context is empty: the reference's eager softmax over
+    nothing but -inf scores is 0 / 0, NaN (torch does the same on a fully
+    masked row); the other rows are untouched by it."""
+    import torch
+
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((2, 4, 8))
+    kp = rng.standard_normal((16, 2, 8))
+    vp = rng.standard_normal((16, 2, 8))
+    table = rng.integers(0, 16, size=(2, 5))
+    out = attend(q, kp, vp, table, np.array([0, 5]), 0.3, 2)
+    assert np.isnan(out[0]).all() and np.isfinite(out[1]).all()
+    scores = torch.full((1, 1, 1, 3), float("-inf"))
+    assert torch.isnan(torch.softmax(scores, dim=-1)).all()

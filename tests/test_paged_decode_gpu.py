@@ -155,3 +155,16 @@ def test_more_sequences_than_a_wave_has_lanes(num_heads, num_kv_heads, head_dim)
     b = PagedBatch(ctx, dtype=torch.bfloat16, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
                    num_slots=8192, seed=31)
     assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize("kernel", ["auto", "equal_splits", "generic"])
+def test_a_row_with_no_keys_is_nan_like_the_reference(kernel):
+    """A context of 0 keys: the reference's softmax over nothing gives 0 / 0
+    (NaN) for that row; the other rows are unaffected."""
+    b = PagedBatch([300, 0, 45], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128, num_slots=2048,
+                   seed=9)
+    out = paged_decode(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.scaling, b.groups,
+                       num_splits=2 if kernel == "equal_splits" else None, kernel=kernel)
+    assert torch.isnan(out[1].float()).all()
+    want = b.oracle()
+    assert_within(out[[0, 2]], want[[0, 2]], 2e-2, 2e-3)

@@ -132,3 +132,34 @@ def test_more_sequences_than_the_work_list_kernel_has_threads(num_heads, num_kv_
                    num_kv_heads=num_kv_heads, head_dim=128, num_slots=65536, seed=21)
     assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
     assert_within(_run(b, one_query_rows=False), b.oracle(), 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize("one_query_rows", [None, False])
+@pytest.mark.parametrize("pool", ["bf16", "fp8"])
+def test_a_packed_pass_writes_its_rows_and_nothing_around_them(one_query_rows, pool):
+    """Chunks beside one-query rows (one of them with a context of one key),
+    into an output that is a window of a larger buffer: every row outside the
+    window keeps its sentinel, bit for bit (no kernel of the pass may store
+    outside the rows it owns)."""
+    from oracle import fp8
+
+    b = PagedBatch([1, 40, 300, 129, 64, 700], [1, 33, 200, 1, 64, 31], dtype=torch.bfloat16, num_heads=32,
+                   num_kv_heads=8, head_dim=128, num_slots=4096, seed=13)
+    kp, vp, k_scale, v_scale = b.key_pool, b.value_pool, 1.0, 1.0
+    if pool == "fp8":
+        k_scale, v_scale = 0.5, 0.25
+        kp = torch.from_numpy(fp8.quantize(to_numpy(b.key_pool), k_scale)).cuda().view(torch.float8_e4m3fn)
+        vp = torch.from_numpy(fp8.quantize(to_numpy(b.value_pool), v_scale)).cuda().view(torch.float8_e4m3fn)
+    t = b.query.shape[0]
+    big = torch.full((t + 8, 32, 128), 7.0, dtype=torch.bfloat16, device="cuda")
+    out = big[4:4 + t]
+    got = paged_prefill(b.query, kp, vp, b.slot_table, b.context_lens_t, b.query_start_loc, max(b.query_lens),
+                        b.scaling, b.groups, one_query_rows=one_query_rows, k_scale=k_scale, v_scale=v_scale,
+                        out=out)
+    torch.cuda.synchronize()
+    assert got.data_ptr() == out.data_ptr()
+    assert torch.equal(big[:4], torch.full_like(big[:4], 7.0))
+    assert torch.equal(big[4 + t:], torch.full_like(big[4 + t:], 7.0))
+    if pool == "bf16":
+        assert_within(got, b.oracle(), 2 ** -6, 2e-3)
+    assert torch.isfinite(got.float()).all()
