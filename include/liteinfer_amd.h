@@ -225,6 +225,33 @@ int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q_stride_hea
                        size_t workspace_bytes, int dtype, int kv_dtype,
                        float k_scale, float v_scale, int flags, void* stream);
 
+/* Bytes of device scratch li_paged_decode_noalloc holds per GPU. */
+#define LI_DECODE_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * li_paged_decode for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference. Same arguments, meaning, kernels and
+ * results as li_paged_decode, without the workspace: the partials live in a
+ * device array of the library, LI_DECODE_NOALLOC_SCRATCH_BYTES on every GPU
+ * it runs on (held until the process ends). A call whose plan
+ * (li_paged_decode_plan) needs more returns LI_EWORKSPACE and launches
+ * nothing. Nothing is allocated, not by the library nor by anything it
+ * calls. Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race; calls in one
+ * stream order are safe. Nothing in the array has to start zeroed.
+ */
+int li_paged_decode_noalloc(const void* q, int64_t q_stride_seq,
+                            int64_t q_stride_head, const void* key_pool,
+                            const void* value_pool, int64_t pool_stride_slot,
+                            int64_t pool_stride_head, const int64_t* slot_table,
+                            int64_t slot_table_stride, int max_context,
+                            const int32_t* context_lens, void* out,
+                            int64_t out_stride_seq, int64_t out_stride_head,
+                            int batch, int num_heads, int num_kv_heads,
+                            int head_dim, float scale, int num_splits,
+                            int block_kv, int dtype, int flags, void* stream);
+
 /*
  * Workspace bytes li_paged_prefill needs for a pass of `batch` sequences over
  * a slot table `max_context` wide on a device of `num_cus` compute units

@@ -22,6 +22,9 @@ LI_FLAG_FORCE_GENERIC = 1
 LI_FLAG_EQUAL_SPLITS = 2
 LI_FLAG_PREFILL_ONLY = 4
 
+# Device scratch li_paged_decode_noalloc holds per GPU (include/liteinfer_amd.h).
+DECODE_NOALLOC_SCRATCH_BYTES = 32 << 20
+
 DTYPE_CODES = {torch.float32: LI_F32, torch.float16: LI_F16, torch.bfloat16: LI_BF16}
 
 # The pool element type of a quantised cache (OCP e4m3: what gfx950's fp8
@@ -40,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "li_paged_decode_plan",
     "li_paged_decode",
     "li_paged_decode_ex",
+    "li_paged_decode_noalloc",
     "li_paged_prefill_plan",
     "li_paged_prefill",
     "li_paged_prefill_ex",
@@ -84,6 +88,11 @@ _SIGNATURES = {
         _i32,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _f32, _f32, _i32, _p],
+    ),
+    "li_paged_decode_noalloc": (
+        _i32,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
+         _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _p],
     ),
     "li_paged_prefill_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)]),
     "li_paged_prefill": (

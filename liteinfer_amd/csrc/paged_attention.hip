@@ -5,6 +5,7 @@
 #include <cmath>
 
 #include <cstdlib>
+#include <mutex>
 
 namespace li {
 namespace {
@@ -303,6 +304,72 @@ extern "C" int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q
                            slot_table, slot_table_stride, max_context, context_lens, out, out_stride_seq,
                            out_stride_head, batch, num_heads, num_kv_heads, head_dim, scale, num_splits, block_kv,
                            workspace, workspace_bytes, dtype, kv_dtype, k_scale, v_scale, flags, stream);
+}
+
+// The no-allocation decode: the workspace li_paged_decode would take lives in
+// a device array of this file (every GPU the library runs on holds its own
+// copy until the process ends). In host code the array's name stands for no
+// device address, so it is only ever reached through the address
+// hipGetSymbolAddress reports, looked up once per device and kept.
+static __device__ __align__(256) char g_decode_scratch[LI_DECODE_NOALLOC_SCRATCH_BYTES];
+
+namespace li {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices];
+
+// This device's copy of g_decode_scratch, or nullptr (and the error set).
+void* decode_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(LI_ELAUNCH, "li_paged_decode_noalloc: no current HIP device");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(g_decode_scratch));
+    if (rc != hipSuccess || !p) {
+      fail(LI_ELAUNCH, "li_paged_decode_noalloc: scratch address on device %d: %s", dev, hipGetErrorString(rc));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+}  // namespace li
+
+extern "C" int li_paged_decode_noalloc(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+                                       const void* key_pool, const void* value_pool, int64_t pool_stride_slot,
+                                       int64_t pool_stride_head, const int64_t* slot_table,
+                                       int64_t slot_table_stride, int max_context, const int32_t* context_lens,
+                                       void* out, int64_t out_stride_seq, int64_t out_stride_head, int batch,
+                                       int num_heads, int num_kv_heads, int head_dim, float scale, int num_splits,
+                                       int block_kv, int dtype, int flags, void* stream) {
+  clear_error();
+  if (int rc = check_common(dtype, num_heads, num_kv_heads, head_dim, "li_paged_decode_noalloc")) return rc;
+  if (num_splits < 0) return fail(LI_EINVAL, "num_splits must be >= 1, got %d", num_splits);
+  if (batch < 0 || max_context < 0) return fail(LI_EINVAL, "li_paged_decode_noalloc: negative extent");
+  if (batch == 0) return LI_OK;
+  size_t need = 0;
+  if (int rc = li_paged_decode_plan(batch, num_heads, num_kv_heads, head_dim, max_context, num_splits, 0, block_kv,
+                                    nullptr, nullptr, &need))
+    return rc;
+  if (need > (size_t)LI_DECODE_NOALLOC_SCRATCH_BYTES)
+    return fail(LI_EWORKSPACE,
+                "li_paged_decode_noalloc: this call needs %zu bytes of scratch, more than the %zu the library "
+                "holds; use li_paged_decode with a workspace",
+                need, (size_t)LI_DECODE_NOALLOC_SCRATCH_BYTES);
+  void* scratch = decode_scratch();
+  if (!scratch) return LI_ELAUNCH;
+  return paged_decode_impl(q, q_stride_seq, q_stride_head, key_pool, value_pool, pool_stride_slot, pool_stride_head,
+                           slot_table, slot_table_stride, max_context, context_lens, out, out_stride_seq,
+                           out_stride_head, batch, num_heads, num_kv_heads, head_dim, scale, num_splits, block_kv,
+                           scratch, (size_t)LI_DECODE_NOALLOC_SCRATCH_BYTES, dtype, dtype, 1.f, 1.f, flags, stream);
 }
 
 // Workspace of the MFMA prefill path: the balanced decode kernel's partials

@@ -316,6 +316,49 @@ def paged_decode(
     return out
 
 
+def paged_decode_noalloc(
+    query: torch.Tensor,
+    key_pool: torch.Tensor,
+    value_pool: torch.Tensor,
+    slot_table: torch.Tensor,
+    context_lens: torch.Tensor,
+    scaling: float,
+    num_kv_groups: int,
+    block_kv: int = _BLOCK_KV,
+    num_splits: int | None = None,
+    *,
+    out: torch.Tensor,
+    kernel: str = "auto",
+) -> torch.Tensor:
+    """`paged_decode` through the entry point that allocates nothing
+    (``li_paged_decode_noalloc``): the partials live in a device array the
+    library holds, so the call needs no workspace. ``out`` (``[batch,
+    num_heads, head_dim]``, the query's dtype, last axis contiguous) receives
+    the result. Raises ValueError when the call needs more scratch than the
+    library holds. Calls that overlap on one GPU share the scratch and race.
+    No counterpart in the reference.
+    """
+    device, query, slot_table, context_lens, kv_code = _decode_inputs(
+        query, key_pool, value_pool, slot_table, context_lens, num_kv_groups, num_splits, 1.0, 1.0)
+    if kv_code != _native.dtype_code(query.dtype):
+        raise ValueError("paged_decode_noalloc takes a pool of the query's dtype")
+    if out.shape != query.shape or out.dtype != query.dtype or out.device != query.device or out.stride(-1) != 1:
+        raise ValueError("out must match the query's shape, dtype and device, with a contiguous last axis")
+    batch, num_heads, head_dim = query.shape
+    lib = _native.load()
+    status = lib.li_paged_decode_noalloc(
+        query.data_ptr(), query.stride(0), query.stride(1),
+        key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
+        slot_table.data_ptr(), slot_table.stride(0), slot_table.shape[1],
+        context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+        batch, num_heads, key_pool.shape[1], head_dim, float(scaling),
+        num_splits or 0, block_kv, _native.dtype_code(query.dtype), _flags(kernel),
+        _native.stream_handle(device),
+    )
+    _native.check(status, "paged_decode_noalloc")
+    return out
+
+
 def paged_prefill(
     query: torch.Tensor,
     key_pool: torch.Tensor,
