@@ -160,9 +160,12 @@ int li_rope_kv_write_fp8(const void* q, const int64_t* q_strides, const void* k,
 /*
  * How many partitions each sequence's key loop is cut into for a decode step
  * of `batch` rows over a slot table `max_context` wide, on a device of
- * `num_cus` compute units (0 = ask the current device). Counterpart of
- * choose_num_splits (liteinfer/models/paged_kernels.py:645-693), tuned for
- * MI355X. Returns the count (>= 1) or a negative error.
+ * `num_cus` compute units (0 = ask the current device). The reference's
+ * choose_num_splits (liteinfer/models/paged_kernels.py:645-693) with CUs for
+ * SMs: 1 under four `block_kv` tiles (0 = 64), else
+ * max(1, min(2 * num_cus / (batch * num_kv_heads), tiles, 32)). Returns the
+ * count (>= 1) or a negative error. (li_paged_decode's num_splits = 0 uses
+ * the library's own fixed-length partitions instead.)
  */
 int li_choose_num_splits(int batch, int num_kv_heads, int max_context,
                          int num_cus, int block_kv);

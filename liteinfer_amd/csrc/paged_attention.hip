@@ -146,15 +146,28 @@ int check_common(int dtype, int num_heads, int num_kv_heads, int head_dim, const
 
 using namespace li;
 
+// The reference's split-count rule (liteinfer/models/paged_kernels.py:
+// 645-693, constants :129-150), with compute units in place of SMs: a
+// context of fewer than four key tiles is not cut; otherwise the count that
+// brings the grid of batch * num_kv_heads programs up to two per CU, at most
+// one per key tile and at most 32. An empty batch takes 1 (the reference
+// would divide by zero).
+constexpr int kRefTargetProgramsPerCu = 2;
+constexpr int kRefMaxSplits = 32;
+constexpr int kRefMinTilesToSplit = 4;
+
 extern "C" int li_choose_num_splits(int batch, int num_kv_heads, int max_context, int num_cus, int block_kv) {
   clear_error();
   if (batch < 0 || num_kv_heads <= 0 || max_context < 0)
     return fail(LI_EINVAL, "li_choose_num_splits: bad extents (batch=%d kv_heads=%d max_context=%d)", batch,
                 num_kv_heads, max_context);
   if (num_cus <= 0) num_cus = device_cu_count();
-  int parts, plen;
-  decode_policy(batch, num_kv_heads, max_context, num_cus, block_kv, &parts, &plen);
-  return parts;
+  const int tile = block_kv > 0 ? block_kv : kDefaultBlockKv;
+  const int64_t tiles = cdiv64(max_context, tile);
+  if (tiles < kRefMinTilesToSplit || batch == 0) return 1;
+  const int64_t programs = (int64_t)batch * num_kv_heads;
+  const int64_t target = (int64_t)kRefTargetProgramsPerCu * num_cus;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(target / programs, tiles), kRefMaxSplits));
 }
 
 extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,

@@ -40,11 +40,11 @@ _BLOCK_KV = 64
 _PREFILL_BLOCK_Q = 16
 _PREFILL_BLOCK_KV = 32
 
-# Partitions one sequence's decode key loop may be cut into. The reference
-# caps this at 32 (paged_kernels.py:129) because its combine holds every
-# split in registers; here the combine streams them, and a 128k-token context
-# wants far more than 32 partitions to fill 256 CUs.
-_MAX_SPLITS = 1024
+# The most programs choose_num_splits cuts one sequence's decode key loop into
+# (the reference's cap, paged_kernels.py:129). The library's own schedules
+# (the balanced split, and the fixed-length partitions of num_splits=None on
+# the general-shape kernel) are not bound by it.
+_MAX_SPLITS = 32
 
 # Compute units assumed when no device is visible (MI355X: 8 XCDs x 32 CUs).
 _MI355X_COMPUTE_UNITS = 256
@@ -80,17 +80,18 @@ def choose_num_splits(
     block_kv: int = _BLOCK_KV,
     num_cus: int | None = None,
 ) -> int:
-    """How many partitions each sequence's decode key loop is cut into.
+    """How many programs to cut each sequence's decode key loop into.
 
-    The counterpart of the reference's chooser (paged_kernels.py:645-693) for
-    MI355X, computed by the library (`li_choose_num_splits`) so the Python and
-    C callers agree. The unsplit grid is one wave per (sequence, KV head);
-    when that cannot keep 256 CUs streaming, each sequence's keys are cut
-    into fixed-length partitions — at most 1024 keys each, at least one
-    `block_kv` tile — until the grid holds about eight waves per CU. A context
-    under four tiles is never cut, and a grid that is already full is not
-    either. The answer is a function of host integers only (`max_context` is
-    the slot table's width), so a captured graph keeps the count it recorded.
+    The reference's rule (paged_kernels.py:645-693), computed by the library
+    (`li_choose_num_splits`) with the device's compute units for SMs: a
+    context of fewer than four `block_kv` tiles is not cut; otherwise the
+    count that brings the grid of ``batch * num_kv_heads`` programs up to two
+    per CU, at most one per tile and at most `_MAX_SPLITS`. The answer is a
+    function of host integers only (`max_context` is the slot table's width),
+    so a captured graph keeps the count it recorded. On bf16 / fp16 the
+    decode kernel takes it as a scheduling hint (its balanced split runs
+    whatever the count); the general-shape kernel and ``kernel="equal_splits"``
+    cut each context into that many equal slices, as the reference does.
     """
     if num_cus is None:
         num_cus = _compute_unit_count(device_index)

@@ -35,9 +35,11 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert hasattr(lib, name), name
 
 
-def _splits(batch, kv_heads, max_context, cus=256):
-    return choose_num_splits(batch, kv_heads, max_context, device_index=0, block_kv=64, num_cus=cus)
+def _splits(batch, kv_heads, max_context, cus=256, block_kv=64):
+    return choose_num_splits(batch, kv_heads, max_context, device_index=0, block_kv=block_kv, num_cus=cus)
 
+
+# The reference's own properties of its chooser (tests/unit/test_paged_decode.py:252-281).
 
 def test_a_batch_that_already_fills_the_device_is_not_split():
     assert _splits(batch=256, kv_heads=8, max_context=1024) == 1
@@ -48,14 +50,14 @@ def test_a_single_sequence_splits_its_key_loop():
 
 
 def test_the_split_count_never_exceeds_the_cap():
-    assert _splits(batch=1, kv_heads=1, max_context=1 << 20) <= _MAX_SPLITS
+    assert _splits(batch=1, kv_heads=1, max_context=1 << 20) <= _MAX_SPLITS == 32
 
 
 def test_a_context_with_too_little_to_cut_is_not_split():
     assert _splits(batch=1, kv_heads=1, max_context=128) == 1
 
 
-def test_no_partition_is_shorter_than_one_key_tile():
+def test_no_split_is_finer_than_one_key_tile():
     assert _splits(batch=1, kv_heads=1, max_context=256) == 4
 
 
@@ -63,11 +65,35 @@ def test_a_longer_context_is_cut_more_finely():
     assert _splits(batch=1, kv_heads=8, max_context=4096) > _splits(batch=1, kv_heads=8, max_context=256)
 
 
-def test_partitions_never_exceed_1024_keys_so_waves_carry_equal_work():
-    # Llama-3-8B decode at batch 64 over contexts up to 8192: 8 partitions of 1024.
-    assert _splits(batch=64, kv_heads=8, max_context=8192) == 8
-    # batch 8 over 131072: 128 partitions of 1024.
-    assert _splits(batch=8, kv_heads=8, max_context=131072) == 128
+# Values the reference's chooser gives, worked by hand from paged_kernels.py:683-693
+# (tiles = cdiv(W, 64); 1 under 4 tiles; else max(1, min(2 * CUs // (B * Hkv), tiles, 32))).
+@pytest.mark.parametrize(
+    ("batch", "kv_heads", "max_context", "cus", "want"),
+    [
+        (1, 8, 4096, 256, 32),     # 512 // 8 = 64, tiles 64, capped at 32
+        (1, 8, 4096, 84, 21),      # an 84-SM A40: 168 // 8 = 21 (docs/benchmarks.md's 21 splits)
+        (4, 8, 8192, 256, 16),     # 512 // 32
+        (64, 8, 8192, 256, 1),     # 512 // 512
+        (12, 8, 4096, 84, 1),      # 168 // 96: "from batch 12 up nothing is split"
+        (8, 8, 256, 84, 2),        # 168 // 64 = 2, tiles 4: the batch-8, 256-token case
+        (1, 1, 255, 256, 4),       # tiles = cdiv(255, 64) = 4
+        (1, 1, 192, 256, 1),       # 3 tiles: under the minimum
+        (3, 2, 100000, 256, 32),   # 512 // 6 = 85, capped
+        (300, 8, 8192, 256, 1),    # target // programs = 0, floored at 1
+    ],
+)
+def test_choose_num_splits_is_the_reference_rule(batch, kv_heads, max_context, cus, want):
+    assert _splits(batch, kv_heads, max_context, cus=cus) == want
+
+
+def test_choose_num_splits_follows_the_tile_size():
+    # 4 tiles of 32 keys are worth cutting; as tiles of 64 they are 2.
+    assert _splits(batch=1, kv_heads=1, max_context=128, block_kv=32) == 4
+    assert _splits(batch=1, kv_heads=1, max_context=128, block_kv=64) == 1
+
+
+def test_choose_num_splits_of_an_empty_batch_is_one():
+    assert _splits(batch=0, kv_heads=8, max_context=4096) == 1
 
 
 def _plan(**kw):
