@@ -84,24 +84,32 @@ class KVCache:
             self._pool.free(block)
 
     def reserve(self, request_ids: list[str], totals: list[int]) -> None:
-        """Give each sequence blocks for `totals[i]` tokens; all or nothing (kv_cache.py:145-169)."""
-        bs = self._pool.block_size
-        wanted = list(zip(request_ids, totals, strict=True))
-        short = sum(self._blocks_short_of(rid, total) for rid, total in wanted)
-        if short > self._pool.num_free_blocks:
+        """Grow each sequence's block table to cover `totals[i]` tokens, all or nothing.
+
+        The shortfall of every entry is added up first and checked against the
+        pool's free blocks, so a step that cannot be served takes no block
+        (the reference's contract, kv_cache.py:145-169, with its message).
+        """
+        entries = list(zip(request_ids, totals, strict=True))
+        missing = sum(self._missing_blocks(rid, total) for rid, total in entries)
+        free = self._pool.num_free_blocks
+        if missing > free:
             raise BlockPoolExhaustedError(
-                f"KV block pool exhausted: this step needs {short} more blocks and "
-                f"{self._pool.num_free_blocks} of {self._pool.num_blocks} are free. "
+                f"KV block pool exhausted: this step needs {missing} more blocks and "
+                f"{free} of {self._pool.num_blocks} are free. "
                 "Increase num_gpu_blocks or reduce max_num_seqs / max_model_len."
             )
-        for rid, total in wanted:
-            table = self._block_tables.setdefault(rid, [])
-            while len(table) * bs < total:
-                table.append(self._pool.allocate())
+        for rid, total in entries:
+            grow = self._missing_blocks(rid, total)
+            if grow:
+                self._block_tables.setdefault(rid, []).extend(self._pool.allocate() for _ in range(grow))
+            else:
+                self._block_tables.setdefault(rid, [])
 
-    def _blocks_short_of(self, request_id: str, total: int) -> int:
-        held = len(self._block_tables.get(request_id, ()))
-        return max(0, -(-total // self._pool.block_size) - held)
+    def _missing_blocks(self, request_id: str, total: int) -> int:
+        """Blocks `request_id` lacks to hold `total` tokens (0 if it has enough)."""
+        needed = (total + self._pool.block_size - 1) // self._pool.block_size
+        return max(0, needed - len(self._block_tables.get(request_id, ())))
 
     def block_table(self, request_id: str) -> list[int]:
         return self._block_tables[request_id]

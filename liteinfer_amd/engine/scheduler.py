@@ -59,8 +59,41 @@ class SchedulerOutput:
     def is_empty(self) -> bool:
         return not self.seqs
 
+    def take(self, seq: Sequence, tokens: int) -> None:
+        """Put `tokens` of `seq`'s uncomputed tokens into this step."""
+        self.seqs.append(seq)
+        self.num_scheduled_tokens[seq.request_id] = tokens
+
+
+class _Budget:
+    """What is left of one step's token budget."""
+
+    def __init__(self, tokens: int) -> None:
+        self.left = tokens
+
+    @property
+    def spent(self) -> bool:
+        return self.left == 0
+
+    def draw(self, seq: Sequence) -> int:
+        """Tokens granted to `seq` now: all it is owed, or what the budget still has."""
+        owed = seq.num_uncomputed_tokens
+        if owed <= 0:
+            raise RuntimeError(f"{seq.request_id} has no uncomputed token to schedule")
+        grant = min(owed, self.left)
+        self.left -= grant
+        return grant
+
 
 class Scheduler:
+    """Seats (``max_num_seqs``) and a per-step token budget, no preemption.
+
+    A step serves the seated sequences first, oldest first, each with what it
+    is owed or what the budget has left; then, while tokens and seats remain,
+    seats the head of the waiting queue and serves it the same way. A prompt
+    larger than what is left is cut there and resumes next step.
+    """
+
     def __init__(self, max_num_seqs: int, token_budget: int) -> None:
         if max_num_seqs < 1 or token_budget < 1:
             raise ValueError("max_num_seqs and token_budget must be >= 1")
@@ -74,32 +107,28 @@ class Scheduler:
         self.waiting.append(seq)
 
     def schedule(self) -> SchedulerOutput:
-        out = SchedulerOutput()
-        budget = self.token_budget
-        for seq in self.running:
-            if budget == 0:
+        step = SchedulerOutput()
+        budget = _Budget(self.token_budget)
+        for seq in [s for s in self.running if not s.is_finished]:
+            if budget.spent:
                 break
-            if not seq.is_finished:
-                budget -= self._grant(out, seq, budget)
-        while budget > 0 and self.waiting and len(self.running) < self.max_num_seqs:
-            seq = self.waiting.popleft()
-            seq.status = SequenceStatus.RUNNING
-            self.running.append(seq)
-            budget -= self._grant(out, seq, budget)
-        return out
+            step.take(seq, budget.draw(seq))
+        while not budget.spent and self.waiting and len(self.running) < self.max_num_seqs:
+            seq = self._seat(self.waiting.popleft())
+            step.take(seq, budget.draw(seq))
+        return step
 
-    @staticmethod
-    def _grant(out: SchedulerOutput, seq: Sequence, budget: int) -> int:
-        num_tokens = min(seq.num_uncomputed_tokens, budget)
-        assert num_tokens > 0, f"{seq.request_id} was scheduled with nothing to compute"
-        out.seqs.append(seq)
-        out.num_scheduled_tokens[seq.request_id] = num_tokens
-        return num_tokens
+    def _seat(self, seq: Sequence) -> Sequence:
+        seq.status = SequenceStatus.RUNNING
+        self.running.append(seq)
+        return seq
 
     def remove_finished(self) -> list[Sequence]:
-        finished = [s for s in self.running if s.is_finished]
-        self.running = [s for s in self.running if not s.is_finished]
-        return finished
+        done, kept = [], []
+        for seq in self.running:
+            (done if seq.is_finished else kept).append(seq)
+        self.running = kept
+        return done
 
     def has_unfinished(self) -> bool:
-        return bool(self.waiting or self.running)
+        return len(self.waiting) + len(self.running) > 0

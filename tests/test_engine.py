@@ -56,3 +56,34 @@ def test_finished_sequences_leave_and_free_their_slot():
 def test_nonsense_configuration_is_refused():
     with pytest.raises(ValueError):
         Scheduler(max_num_seqs=0, token_budget=8)
+
+
+def test_a_budget_exactly_spent_by_running_sequences_admits_no_one():
+    """The seated sequences take the whole budget: nobody waiting is seated
+    this step (the reference's `budget == 0` break), and a finished sequence
+    in the running list is skipped, not served."""
+    sched = Scheduler(max_num_seqs=4, token_budget=2)
+    a, b, c = (Sequence(r, [1] * 3, max_tokens=5) for r in "abc")
+    for s in (a, b):
+        sched.add(s)
+    first = sched.schedule()                       # a gets 2 of its 3 prompt tokens
+    assert [s.request_id for s in first.seqs] == ["a"] and first.num_scheduled_tokens["a"] == 2
+    a.num_computed_tokens = 2
+    sched.add(c)
+    second = sched.schedule()                      # a finishes its prompt (1), b starts (1)
+    assert second.num_scheduled_tokens == {"a": 1, "b": 1}
+    assert [s.request_id for s in sched.waiting] == ["c"]
+    a.status = SequenceStatus.FINISHED_LENGTH
+    b.num_computed_tokens = 1
+    third = sched.schedule()                       # a skipped; b owes 2, the budget is spent
+    assert third.num_scheduled_tokens == {"b": 2} and len(sched.waiting) == 1
+
+
+def test_a_sequence_with_nothing_to_compute_is_an_error():
+    sched = Scheduler(max_num_seqs=2, token_budget=8)
+    s = Sequence("x", [1, 2], max_tokens=3)
+    sched.add(s)
+    sched.schedule()
+    s.num_computed_tokens = len(s)
+    with pytest.raises(RuntimeError, match="no uncomputed token"):
+        sched.schedule()
