@@ -83,14 +83,17 @@ int li_abi_version(void);
  * k and v are [batch, num_kv_heads, tokens, head_dim] with arbitrary element
  * strides (k_strides / v_strides = {batch, head, token, dim}); slots holds
  * batch*tokens entries in batch-major token order. A bit-exact copy. A slot
- * outside [0, num_slots) is not written (torch's index_put_ would raise).
+ * outside [0, num_slots) is not written (torch's index_put_ would raise;
+ * a kernel cannot): when bad_slots is not NULL, the device int32 it points
+ * to is increased by the number of such tokens, for the caller to read when
+ * it can synchronise (the Python wrapper raises IndexError then).
  */
 int li_kv_scatter(const void* k, const void* v, const int64_t* k_strides,
                   const int64_t* v_strides, int64_t batch, int64_t tokens,
                   const int64_t* slots, void* key_pool, void* value_pool,
                   int64_t num_slots, int64_t pool_stride_slot,
                   int64_t pool_stride_head, int num_kv_heads, int head_dim,
-                  int dtype, void* stream);
+                  int dtype, int32_t* bad_slots, void* stream);
 
 /*
  * Quantising KV slot-write into an fp8 (LI_FP8_E4M3) pool: the reference's
@@ -101,13 +104,15 @@ int li_kv_scatter(const void* k, const void* v, const int64_t* k_strides,
  * (the reciprocal in fp32, round to nearest even), k and v of src_dtype
  * (LI_F32 / LI_F16 / LI_BF16). The readers multiply back by the scale. No
  * counterpart in the reference's code: its cache is never quantised.
+ * bad_slots as for li_kv_scatter.
  */
 int li_kv_scatter_fp8(const void* k, const void* v, const int64_t* k_strides,
                       const int64_t* v_strides, int64_t batch, int64_t tokens,
                       const int64_t* slots, void* key_pool, void* value_pool,
                       int64_t num_slots, int64_t pool_stride_slot,
                       int64_t pool_stride_head, int num_kv_heads, int head_dim,
-                      int src_dtype, float k_scale, float v_scale, void* stream);
+                      int src_dtype, float k_scale, float v_scale,
+                      int32_t* bad_slots, void* stream);
 
 /*
  * Fused rotary embedding + KV slot-write. Replaces, per layer, the
@@ -124,7 +129,8 @@ int li_kv_scatter_fp8(const void* k, const void* v, const int64_t* k_strides,
  * broadcasts). slots holds batch*tokens entries in batch-major token order.
  * Every product and sum is rounded to `dtype` as the separate torch ops round
  * it, so q_out and the pool rows are bit-identical to the reference's
- * sequence. A slot outside [0, num_slots) is not written.
+ * sequence. A slot outside [0, num_slots) is not written, and counted into
+ * *bad_slots when bad_slots is not NULL (as for li_kv_scatter).
  */
 int li_rope_kv_write(const void* q, const int64_t* q_strides, const void* k,
                      const int64_t* k_strides, const void* v,
@@ -135,7 +141,7 @@ int li_rope_kv_write(const void* q, const int64_t* q_strides, const void* k,
                      void* value_pool, int64_t num_slots,
                      int64_t pool_stride_slot, int64_t pool_stride_head,
                      int num_heads, int num_kv_heads, int head_dim, int dtype,
-                     void* stream);
+                     int32_t* bad_slots, void* stream);
 
 /*
  * li_rope_kv_write into fp8 (LI_FP8_E4M3) pools: q_out as li_rope_kv_write
@@ -155,7 +161,8 @@ int li_rope_kv_write_fp8(const void* q, const int64_t* q_strides, const void* k,
                          void* value_pool, int64_t num_slots,
                          int64_t pool_stride_slot, int64_t pool_stride_head,
                          int num_heads, int num_kv_heads, int head_dim, int dtype,
-                         float k_scale, float v_scale, void* stream);
+                         float k_scale, float v_scale, int32_t* bad_slots,
+                         void* stream);
 
 /*
  * How many partitions each sequence's key loop is cut into for a decode step
@@ -193,8 +200,9 @@ int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads,
  *   q   [batch, num_heads, head_dim]   strides (q_stride_seq, q_stride_head, 1)
  *   out [batch, num_heads, head_dim]   strides (out_stride_seq, out_stride_head, 1)
  * Query head h reads KV head h / (num_heads / num_kv_heads). Row i attends
- * to slot_table[i, 0:context_lens[i]]. fp32 accumulation; the output is
- * rounded to `dtype` once. `workspace` must hold the bytes
+ * to slot_table[i, 0:context_lens[i]]. The pools hold fewer than 2^31 slots
+ * (the kernels stage slot indices as 32-bit integers). fp32 accumulation;
+ * the output is rounded to `dtype` once. `workspace` must hold the bytes
  * li_paged_decode_plan reports (it may be NULL when that is 0).
  */
 int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,

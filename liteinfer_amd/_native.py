@@ -57,21 +57,21 @@ _SIGNATURES = {
     "li_abi_version": (_i32, []),
     "li_kv_scatter": (
         _i32,
-        [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p],
+        [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p],
     ),
     "li_kv_scatter_fp8": (
         _i32,
-        [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _f32, _f32, _p],
+        [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _f32, _f32, _p, _p],
     ),
     "li_rope_kv_write": (
         _i32,
         [_p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64p, _i64, _i64, _p, _p, _i64p, _p, _p,
-         _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p],
+         _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p, _p],
     ),
     "li_rope_kv_write_fp8": (
         _i32,
         [_p, _i64p, _p, _i64p, _p, _i64p, _p, _p, _i64p, _i64, _i64, _p, _p, _i64p, _p, _p,
-         _i64, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _f32, _p],
+         _i64, _i64, _i64, _i32, _i32, _i32, _i32, _f32, _f32, _p, _p],
     ),
     "li_choose_num_splits": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "li_paged_decode_plan": (
@@ -107,7 +107,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -71,6 +71,9 @@ class BlockPool:
         self._keys = torch.zeros(shape, dtype=storage, device=device)
         self._values = torch.zeros(shape, dtype=storage, device=device)
         self._free_blocks: list[int] = list(range(num_blocks))
+        # Count of slot writes that named a slot outside the pool. The device
+        # kernels skip such a write and add to this counter instead of raising.
+        self.bad_slots = torch.zeros(1, dtype=torch.int32, device=device)
 
     @property
     def nbytes(self) -> int:
@@ -96,6 +99,18 @@ class BlockPool:
 
     def free(self, block_idx: int) -> None:
         self._free_blocks.append(block_idx)
+
+    def check_slot_writes(self) -> None:
+        """Raise IndexError if any slot write since the last check missed the pool.
+
+        Reads a device counter, so it waits for the writes already queued;
+        call it where the caller synchronises anyway, never under capture.
+        """
+        missed = int(self.bad_slots.item())
+        if missed:
+            self.bad_slots.zero_()
+            raise IndexError(f"{missed} K/V slot writes named a slot outside the pool's "
+                             f"{self.num_blocks * self.block_size} slots and were not stored")
 
     def slots(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
         """This layer's flat key/value stores, ``[num_slots, num_kv_heads, head_dim]``."""

@@ -48,15 +48,18 @@ def quantize_fp8(x: torch.Tensor, scale: float) -> torch.Tensor:
 
 
 def scatter_into(key_pool: torch.Tensor, value_pool: torch.Tensor, slots: torch.Tensor,
-                 k: torch.Tensor, v: torch.Tensor, k_scale: float = 1.0, v_scale: float = 1.0) -> None:
+                 k: torch.Tensor, v: torch.Tensor, k_scale: float = 1.0, v_scale: float = 1.0,
+                 bad_slots: torch.Tensor | None = None) -> None:
     """Store ``[B, H, T, D]`` K/V rows at `slots` (B*T entries, batch-major) of one layer's pools.
 
     An fp8 pool stores each row quantised with its scale (`quantize_fp8`).
+    On the device a slot outside the pool is skipped and counted into
+    `bad_slots`; torch's indexed assignment raises for it on the CPU.
     """
     if key_pool.device.type == "cuda":
         from liteinfer_amd.paged_kernels import kv_scatter
 
-        kv_scatter(key_pool, value_pool, slots, k, v, k_scale=k_scale, v_scale=v_scale)
+        kv_scatter(key_pool, value_pool, slots, k, v, k_scale=k_scale, v_scale=v_scale, bad_slots=bad_slots)
         return
     flat = slots.reshape(-1)
     if key_pool.dtype == torch.float8_e4m3fn:
@@ -147,7 +150,7 @@ class KVCache:
     def scatter(self, layer_idx: int, slots: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         """Store one K/V column per slot, in the order the pass holds its tokens (kv_cache.py:236-247)."""
         keys, values = self._pool.slots(layer_idx)
-        scatter_into(keys, values, slots, k, v, self._pool.k_scale, self._pool.v_scale)
+        scatter_into(keys, values, slots, k, v, self._pool.k_scale, self._pool.v_scale, self._pool.bad_slots)
 
     def rotate_and_scatter(self, layer_idx: int, slots: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
                            v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -161,7 +164,8 @@ class KVCache:
             from liteinfer_amd.rope import rope_kv_write
 
             return rope_kv_write(q, k, v, cos, sin, slots, keys, values,
-                                 k_scale=self._pool.k_scale, v_scale=self._pool.v_scale)
+                                 k_scale=self._pool.k_scale, v_scale=self._pool.v_scale,
+                                 bad_slots=self._pool.bad_slots)
         from liteinfer_amd.rope import apply_rotary_pos_emb
 
         q_embed, k_embed = apply_rotary_pos_emb(q, k, cos, sin)

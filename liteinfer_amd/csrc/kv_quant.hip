@@ -36,6 +36,7 @@ struct QuantArgs {
   int heads;
   int head_dim;
   float inv_k, inv_v;
+  int* bad;  // nullable: counts tokens whose slot is out of range
 };
 
 template <typename E>
@@ -94,7 +95,10 @@ __global__ __launch_bounds__(256) void kv_quant_vec16(QuantArgs a) {
     const int h = rem / units;
     const int u = rem - h * units;
     const int64_t slot = a.slots[i];
-    if (slot < 0 || slot >= a.num_slots) continue;
+    if (slot < 0 || slot >= a.num_slots) {
+      if (rem == 0 && a.bad) atomicAdd(a.bad, 1);
+      continue;
+    }
     const int64_t b = i / a.tokens, t = i - b * a.tokens;
     const int64_t d = (int64_t)u * 16;
     const E* ksrc = reinterpret_cast<const E*>(a.k) + b * a.ks[0] + h * a.ks[1] + t * a.ks[2] + d;
@@ -117,7 +121,10 @@ __global__ __launch_bounds__(256) void kv_quant_elem(QuantArgs a) {
     const int h = rem / a.head_dim;
     const int d = rem - h * a.head_dim;
     const int64_t slot = a.slots[i];
-    if (slot < 0 || slot >= a.num_slots) continue;
+    if (slot < 0 || slot >= a.num_slots) {
+      if (rem == 0 && a.bad) atomicAdd(a.bad, 1);
+      continue;
+    }
     const int64_t b = i / a.tokens, t = i - b * a.tokens;
     const float kx = to_f32(reinterpret_cast<const E*>(a.k)[b * a.ks[0] + h * a.ks[1] + t * a.ks[2] + d * a.ks[3]]);
     const float vx = to_f32(reinterpret_cast<const E*>(a.v)[b * a.vs[0] + h * a.vs[1] + t * a.vs[2] + d * a.vs[3]]);
@@ -151,7 +158,7 @@ extern "C" int li_kv_scatter_fp8(const void* k, const void* v, const int64_t* k_
                                  int64_t batch, int64_t tokens, const int64_t* slots, void* key_pool,
                                  void* value_pool, int64_t num_slots, int64_t pool_stride_slot,
                                  int64_t pool_stride_head, int num_kv_heads, int head_dim, int src_dtype,
-                                 float k_scale, float v_scale, void* stream) {
+                                 float k_scale, float v_scale, int32_t* bad_slots, void* stream) {
   li::clear_error();
   if (src_dtype != LI_F32 && src_dtype != LI_F16 && src_dtype != LI_BF16)
     return li::fail(LI_EINVAL, "li_kv_scatter_fp8: unknown source dtype %d", src_dtype);
@@ -188,6 +195,7 @@ extern "C" int li_kv_scatter_fp8(const void* k, const void* v, const int64_t* k_
   a.head_dim = head_dim;
   a.inv_k = 1.f / k_scale;
   a.inv_v = 1.f / v_scale;
+  a.bad = bad_slots;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int esize = li::dtype_size(src_dtype);

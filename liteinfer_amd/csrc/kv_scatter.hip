@@ -27,6 +27,7 @@ struct ScatterArgs {
   int heads;
   int head_dim;
   int esize;  // bytes per element
+  int* bad;   // nullable: counts tokens whose slot is out of range
 };
 
 // 16-byte units: the row of one head is head_dim * esize / 16 units.
@@ -42,7 +43,10 @@ __global__ __launch_bounds__(256) void kv_scatter_vec16(ScatterArgs a) {
     const int h = rem / units;
     const int u = rem - h * units;
     const int64_t slot = a.slots[i];
-    if (slot < 0 || slot >= a.num_slots) continue;
+    if (slot < 0 || slot >= a.num_slots) {
+      if (rem == 0 && a.bad) atomicAdd(a.bad, 1);
+      continue;
+    }
     const int64_t b = i / a.tokens, t = i - b * a.tokens;
     const int64_t d = (int64_t)u * epu;
     const int64_t ko = b * a.ks[0] + h * a.ks[1] + t * a.ks[2] + d;
@@ -67,7 +71,10 @@ __global__ __launch_bounds__(256) void kv_scatter_elem(ScatterArgs a) {
     const int h = rem / a.head_dim;
     const int d = rem - h * a.head_dim;
     const int64_t slot = a.slots[i];
-    if (slot < 0 || slot >= a.num_slots) continue;
+    if (slot < 0 || slot >= a.num_slots) {
+      if (rem == 0 && a.bad) atomicAdd(a.bad, 1);
+      continue;
+    }
     const int64_t b = i / a.tokens, t = i - b * a.tokens;
     const int64_t ko = b * a.ks[0] + h * a.ks[1] + t * a.ks[2] + d * a.ks[3];
     const int64_t vo = b * a.vs[0] + h * a.vs[1] + t * a.vs[2] + d * a.vs[3];
@@ -94,7 +101,7 @@ extern "C" int li_kv_scatter(const void* k, const void* v, const int64_t* k_stri
                              const int64_t* slots, void* key_pool, void* value_pool,
                              int64_t num_slots, int64_t pool_stride_slot,
                              int64_t pool_stride_head, int num_kv_heads, int head_dim,
-                             int dtype, void* stream) {
+                             int dtype, int32_t* bad_slots, void* stream) {
   li::clear_error();
   const int esize = li::dtype_size(dtype);
   if (esize == 0) return li::fail(LI_EINVAL, "li_kv_scatter: unknown dtype %d", dtype);
@@ -128,6 +135,7 @@ extern "C" int li_kv_scatter(const void* k, const void* v, const int64_t* k_stri
   a.heads = num_kv_heads;
   a.head_dim = head_dim;
   a.esize = esize;
+  a.bad = bad_slots;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int threads = 256;

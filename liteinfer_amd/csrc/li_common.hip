@@ -50,4 +50,4 @@ int device_cu_count() {
 
 extern "C" const char* li_last_error_string(void) { return li::g_last_error.c_str(); }
 
-extern "C" int li_abi_version(void) { return 4; }
+extern "C" int li_abi_version(void) { return 5; }

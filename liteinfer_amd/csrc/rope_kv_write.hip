@@ -49,6 +49,7 @@ struct RopeArgs {
   int64_t ps_slot, ps_head;
   int num_heads, num_kv_heads, head_dim;
   float inv_k, inv_v;  // fp8 pools: 1 / k_scale, 1 / v_scale
+  int* bad;            // nullable: counts tokens whose slot is out of range
 };
 
 // Eight values, rounded to E (as stored by the unfused path), to eight e4m3
@@ -151,7 +152,10 @@ __global__ __launch_bounds__(256) void rope_kv_write_vec(RopeArgs a) {
       dst = reinterpret_cast<E*>(a.qo) + b * a.os[0] + h * a.os[1] + t * a.os[2] + d0;
     } else {
       const int64_t slot = a.slots[i];
-      if (slot < 0 || slot >= a.num_slots) continue;
+      if (slot < 0 || slot >= a.num_slots) {
+        if (h == 0 && d0 == 0 && a.bad) atomicAdd(a.bad, 1);
+        continue;
+      }
       if constexpr (F8) dst8 = reinterpret_cast<uint8_t*>(a.kp) + slot * a.ps_slot + h * a.ps_head + d0;
       else dst = reinterpret_cast<E*>(a.kp) + slot * a.ps_slot + h * a.ps_head + d0;
     }
@@ -216,7 +220,10 @@ __global__ __launch_bounds__(256) void rope_kv_write_elem(RopeArgs a) {
       od = a.os[3];
     } else {
       const int64_t slot = a.slots[i];
-      if (slot < 0 || slot >= a.num_slots) continue;
+      if (slot < 0 || slot >= a.num_slots) {
+        if (h == 0 && d == 0 && a.bad) atomicAdd(a.bad, 1);
+        continue;
+      }
       src = reinterpret_cast<const E*>(a.k) + b * a.ks[0] + h * a.ks[1] + t * a.ks[2];
       sd = a.ks[3];
       dst = reinterpret_cast<E*>(a.kp) + slot * a.ps_slot + h * a.ps_head;
@@ -260,7 +267,8 @@ int rope_impl(const void* q, const int64_t* q_strides, const void* k, const int6
               const int64_t* v_strides, const void* cos, const void* sin, const int64_t* cs_strides, int64_t batch,
               int64_t tokens, const int64_t* slots, void* q_out, const int64_t* q_out_strides, void* key_pool,
               void* value_pool, int64_t num_slots, int64_t pool_stride_slot, int64_t pool_stride_head, int num_heads,
-              int num_kv_heads, int head_dim, int dtype, bool fp8, float k_scale, float v_scale, void* stream) {
+              int num_kv_heads, int head_dim, int dtype, bool fp8, float k_scale, float v_scale, int32_t* bad_slots,
+              void* stream) {
   li::clear_error();
   const int esize = li::dtype_size(dtype);
   if (esize == 0) return li::fail(LI_EINVAL, "li_rope_kv_write: unknown dtype %d", dtype);
@@ -311,6 +319,7 @@ int rope_impl(const void* q, const int64_t* q_strides, const void* k, const int6
   a.head_dim = head_dim;
   a.inv_k = fp8 ? 1.f / k_scale : 1.f;
   a.inv_v = fp8 ? 1.f / v_scale : 1.f;
+  a.bad = bad_slots;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int threads = 256;
@@ -361,10 +370,10 @@ extern "C" int li_rope_kv_write(const void* q, const int64_t* q_strides, const v
                                 const int64_t* cs_strides, int64_t batch, int64_t tokens, const int64_t* slots,
                                 void* q_out, const int64_t* q_out_strides, void* key_pool, void* value_pool,
                                 int64_t num_slots, int64_t pool_stride_slot, int64_t pool_stride_head, int num_heads,
-                                int num_kv_heads, int head_dim, int dtype, void* stream) {
+                                int num_kv_heads, int head_dim, int dtype, int32_t* bad_slots, void* stream) {
   return rope_impl(q, q_strides, k, k_strides, v, v_strides, cos, sin, cs_strides, batch, tokens, slots, q_out,
                    q_out_strides, key_pool, value_pool, num_slots, pool_stride_slot, pool_stride_head, num_heads,
-                   num_kv_heads, head_dim, dtype, false, 1.f, 1.f, stream);
+                   num_kv_heads, head_dim, dtype, false, 1.f, 1.f, bad_slots, stream);
 }
 
 extern "C" int li_rope_kv_write_fp8(const void* q, const int64_t* q_strides, const void* k,
@@ -373,8 +382,8 @@ extern "C" int li_rope_kv_write_fp8(const void* q, const int64_t* q_strides, con
                                     int64_t tokens, const int64_t* slots, void* q_out, const int64_t* q_out_strides,
                                     void* key_pool, void* value_pool, int64_t num_slots, int64_t pool_stride_slot,
                                     int64_t pool_stride_head, int num_heads, int num_kv_heads, int head_dim, int dtype,
-                                    float k_scale, float v_scale, void* stream) {
+                                    float k_scale, float v_scale, int32_t* bad_slots, void* stream) {
   return rope_impl(q, q_strides, k, k_strides, v, v_strides, cos, sin, cs_strides, batch, tokens, slots, q_out,
                    q_out_strides, key_pool, value_pool, num_slots, pool_stride_slot, pool_stride_head, num_heads,
-                   num_kv_heads, head_dim, dtype, true, k_scale, v_scale, stream);
+                   num_kv_heads, head_dim, dtype, true, k_scale, v_scale, bad_slots, stream);
 }

@@ -80,6 +80,7 @@ class LLM:
             if sample:
                 rows = torch.tensor(sample, device=logits.device)
                 tokens = logits.index_select(0, rows).argmax(dim=-1).tolist()
+                self.cache.pool.check_slot_writes()
                 for i, tok in zip(sample, tokens):
                     seq = out.seqs[i]
                     seq.output_token_ids.append(int(tok))
@@ -89,6 +90,7 @@ class LLM:
                 self.runner.release(seq)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        self.cache.pool.check_slot_writes()
         stats = GenerateStats(wall, steps, decode_steps, sum(len(p) for p in prompts),
                               sum(len(s.output_token_ids) for s in seqs))
         return [s.output_token_ids for s in seqs], stats

@@ -122,6 +122,17 @@ def _check_pools(key_pool: torch.Tensor, value_pool: torch.Tensor) -> None:
         raise ValueError("key and value pools must share a dtype")
 
 
+_MAX_ATTEND_SLOTS = 1 << 31
+
+
+def _check_attend_pools(key_pool: torch.Tensor, value_pool: torch.Tensor) -> None:
+    """The pools' checks for an attention pass, whose kernels hold slot indices in 32 bits."""
+    _check_pools(key_pool, value_pool)
+    if key_pool.shape[0] >= _MAX_ATTEND_SLOTS:
+        raise ValueError(f"the pools hold {key_pool.shape[0]} slots; paged attention reads pools "
+                         f"of fewer than 2**31 slots")
+
+
 def _kv_dtype_code(query: torch.Tensor, key_pool: torch.Tensor, k_scale: float, v_scale: float) -> int:
     """The pool's element type code: the query's, or fp8 (with checked scales)."""
     if _is_fp8(key_pool):
@@ -152,6 +163,28 @@ def _check_scales(k_scale: float, v_scale: float) -> None:
             raise ValueError(f"{name} must be finite and > 0, got {value}")
 
 
+def bad_slots_pointer(bad_slots: torch.Tensor | None, device: torch.device) -> int | None:
+    """Device address of a slot-write miss counter (None for no counter)."""
+    if bad_slots is None:
+        return None
+    if bad_slots.dtype != torch.int32 or bad_slots.numel() < 1 or bad_slots.device != device:
+        raise ValueError(f"bad_slots must be an int32 tensor of at least one element on {device}, "
+                         f"got {bad_slots.dtype} {tuple(bad_slots.shape)} on {bad_slots.device}")
+    return bad_slots.data_ptr()
+
+
+def check_bad_slots(bad_slots: torch.Tensor) -> None:
+    """Raise IndexError if slot writes counted into `bad_slots` missed the pool; reset it.
+
+    Reading the counter synchronises with the writes already queued, so call
+    it where the caller synchronises anyway (outside captured regions).
+    """
+    missed = int(bad_slots.reshape(-1)[0].item())
+    if missed:
+        bad_slots.zero_()
+        raise IndexError(f"{missed} K/V slot writes named a slot outside the pool and were not stored")
+
+
 def kv_scatter(
     key_pool: torch.Tensor,
     value_pool: torch.Tensor,
@@ -161,6 +194,7 @@ def kv_scatter(
     *,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    bad_slots: torch.Tensor | None = None,
 ) -> None:
     """Store one K/V column per slot, in the order the pass holds its tokens.
 
@@ -171,8 +205,15 @@ def kv_scatter(
     for an fp8 (``torch.float8_e4m3fn``) pool, each element quantised as
     ``e4m3(clamp(x * (1 / scale), +-448))`` with ``k_scale`` / ``v_scale``
     (the reference's planned storage-level quantisation, roadmap section 2.5).
+
+    A slot outside ``[0, num_slots)`` is not written. torch's ``index_put_``
+    raises for it; a kernel cannot, so when `bad_slots` (a one-element int32
+    tensor on the pools' device) is given, the kernel adds the number of such
+    tokens to it, and the caller reads it once it synchronises
+    (`check_bad_slots`).
     """
     device = _require_device_tensors(key_pool, value_pool, slots, k, v)
+    bad_ptr = bad_slots_pointer(bad_slots, device)
     _check_pools(key_pool, value_pool)
     if k.dim() != 4 or k.shape != v.shape:
         raise ValueError(f"k and v must both be [batch, heads, tokens, head_dim], got {tuple(k.shape)}, {tuple(v.shape)}")
@@ -198,7 +239,7 @@ def kv_scatter(
             key_pool.data_ptr(), value_pool.data_ptr(),
             key_pool.shape[0], key_pool.stride(0), key_pool.stride(1),
             heads, head_dim, _native.dtype_code(k.dtype), float(k_scale), float(v_scale),
-            _native.stream_handle(device),
+            bad_ptr, _native.stream_handle(device),
         )
         _native.check(status, "kv_scatter")
         return
@@ -209,7 +250,7 @@ def kv_scatter(
         key_pool.data_ptr(), value_pool.data_ptr(),
         key_pool.shape[0], key_pool.stride(0), key_pool.stride(1),
         heads, head_dim, _native.dtype_code(key_pool.dtype),
-        _native.stream_handle(device),
+        bad_ptr, _native.stream_handle(device),
     )
     _native.check(status, "kv_scatter")
 
@@ -222,7 +263,7 @@ def _decode_inputs(query, key_pool, value_pool, slot_table, context_lens, num_kv
     if num_splits is not None and num_splits < 1:
         raise ValueError(f"num_splits must be >= 1, got {num_splits}")
     device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens)
-    _check_pools(key_pool, value_pool)
+    _check_attend_pools(key_pool, value_pool)
     _, num_heads, head_dim = query.shape
     kv_code = _kv_dtype_code(query, key_pool, k_scale, v_scale)
     if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:
@@ -414,7 +455,7 @@ def paged_prefill(
     if key_pool.stride() != value_pool.stride():
         raise ValueError("key and value pools must be laid out identically")
     device = _require_device_tensors(query, key_pool, value_pool, slot_table, context_lens, query_start_loc)
-    _check_pools(key_pool, value_pool)
+    _check_attend_pools(key_pool, value_pool)
     _, num_heads, head_dim = query.shape
     kv_code = _kv_dtype_code(query, key_pool, k_scale, v_scale)
     if num_heads % num_kv_groups != 0 or num_heads // num_kv_groups != key_pool.shape[1]:

@@ -15,7 +15,7 @@ from __future__ import annotations
 import torch
 
 from liteinfer_amd import _native
-from liteinfer_amd.paged_kernels import _as_index, _check_pools, _require_device_tensors
+from liteinfer_amd.paged_kernels import _as_index, _check_pools, _require_device_tensors, bad_slots_pointer
 
 
 def rotate_half(x: torch.Tensor) -> torch.Tensor:
@@ -44,6 +44,7 @@ def rope_kv_write(
     *,
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    bad_slots: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Rotate q and k, store k and v at `slots`, return the rotated q.
 
@@ -60,6 +61,8 @@ def rope_kv_write(
             (``torch.float8_e4m3fn``) pool stores the rotated k (rounded to
             q's dtype, as the torch ops round it) and v quantised with
             `k_scale` / `v_scale`, exactly as `kv_scatter` would store them.
+        bad_slots: optional one-element int32 counter of slots outside the
+            pool (not written), as for `kv_scatter`.
 
     Returns:
         The rotated q, ``[batch, num_heads, tokens, head_dim]``, laid out
@@ -67,6 +70,7 @@ def rope_kv_write(
         attention's ``squeeze(0).transpose(0, 1)`` is a free view).
     """
     device = _require_device_tensors(q, k, v, cos, sin, slots, key_pool, value_pool)
+    bad_ptr = bad_slots_pointer(bad_slots, device)
     _check_pools(key_pool, value_pool)
     if q.dim() != 4 or k.dim() != 4 or k.shape != v.shape:
         raise ValueError(f"q, k, v must be [batch, heads, tokens, head_dim], got {tuple(q.shape)}, "
@@ -113,8 +117,9 @@ def rope_kv_write(
     if fp8:
         if not (k_scale > 0 and v_scale > 0):
             raise ValueError(f"k_scale and v_scale must be > 0, got {k_scale}, {v_scale}")
-        status = lib.li_rope_kv_write_fp8(*args, float(k_scale), float(v_scale), _native.stream_handle(device))
+        status = lib.li_rope_kv_write_fp8(*args, float(k_scale), float(v_scale), bad_ptr,
+                                          _native.stream_handle(device))
     else:
-        status = lib.li_rope_kv_write(*args, _native.stream_handle(device))
+        status = lib.li_rope_kv_write(*args, bad_ptr, _native.stream_handle(device))
     _native.check(status, "rope_kv_write")
     return out

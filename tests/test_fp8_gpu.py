@@ -241,6 +241,23 @@ def test_fused_rope_write_into_fp8_pools_is_rope_then_quantising_scatter(dtype, 
     assert torch.equal(q_out, q16) and torch.equal(q_out, want_q)
 
 
+def test_fused_rope_write_into_fp8_pools_counts_slots_outside_the_pool():
+    from liteinfer_amd.rope import rope_kv_write
+
+    g = torch.Generator(device=DEV).manual_seed(12)
+    q = torch.randn(1, 8, 4, 128, generator=g, device=DEV).to(torch.bfloat16)
+    k = torch.randn(1, 2, 4, 128, generator=g, device=DEV).to(torch.bfloat16)
+    ang = torch.rand(1, 4, 128, generator=g, device=DEV)
+    cos, sin = ang.cos().to(torch.bfloat16), ang.sin().to(torch.bfloat16)
+    kp = torch.zeros(16, 2, 128, dtype=FP8, device=DEV)
+    vp = torch.zeros_like(kp)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    rope_kv_write(q, k, k, cos, sin, torch.tensor([[2, 16, -3, 5]], device=DEV), kp, vp, bad_slots=bad)
+    assert int(bad.item()) == 2
+    written = (kp.view(torch.uint8) != 0).any(dim=(1, 2)).nonzero().reshape(-1).tolist()
+    assert written == [2, 5]
+
+
 @pytest.mark.parametrize("src_dtype", [torch.bfloat16, torch.float32])
 def test_quantising_slot_write_passes_nan_through(src_dtype):
     """A NaN in K or V is stored as the e4m3 NaN (as torch's cast stores it),

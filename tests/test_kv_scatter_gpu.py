@@ -8,7 +8,7 @@ import torch
 
 from liteinfer_amd.cache.block_pool import BlockPool
 from liteinfer_amd.cache.kv_cache import KVCache, tokens_first
-from liteinfer_amd.paged_kernels import kv_scatter
+from liteinfer_amd.paged_kernels import check_bad_slots, kv_scatter
 from oracle import addressing
 
 pytestmark = pytest.mark.gpu
@@ -90,10 +90,43 @@ def test_out_of_range_slots_are_not_written():
     slots[0, 1] = 64
     slots[0, 2] = -1
     before = _bits(kp)
-    kv_scatter(kp, vp, slots, k, v)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kv_scatter(kp, vp, slots, k, v, bad_slots=bad)
     after = _bits(kp)
     changed = np.nonzero((after != before).any(axis=(1, 2)))[0].tolist()
     assert sorted(changed) == sorted([int(slots[0, 0]), int(slots[0, 3])])
+    assert int(bad.item()) == 2
+    kv_scatter(kp, vp, slots, k, v)  # no counter: the same skip, nothing counted
+    assert int(bad.item()) == 2
+    with pytest.raises(IndexError, match="2 K/V slot writes"):
+        check_bad_slots(bad)
+    assert int(bad.item()) == 0
+    check_bad_slots(bad)
+
+
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float32])
+def test_fp8_out_of_range_slots_are_counted(src):
+    _, _, k, v, slots = _case(1, 2, 4, 16, 64, src)
+    kp = torch.zeros(64, 4, 16, dtype=torch.float8_e4m3fn, device=DEV)
+    vp = torch.zeros_like(kp)
+    slots = slots.clone()
+    slots[0, 0] = 1 << 40
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    kv_scatter(kp, vp, slots, k, v, k_scale=0.5, v_scale=2.0, bad_slots=bad)
+    assert int(bad.item()) == 1
+    written = (kp.view(torch.uint8) != 0).any(dim=(1, 2)).nonzero().reshape(-1).tolist()
+    assert set(written) <= {int(slots[0, 1])}
+
+
+def test_pool_check_slot_writes_raises_after_a_bad_decode_write():
+    pool = BlockPool(num_layers=1, num_blocks=4, block_size=16, num_kv_heads=2, head_dim=64,
+                     dtype=torch.bfloat16, device=DEV)
+    cache = KVCache(pool)
+    k = torch.randn(2, 2, 1, 64, dtype=torch.bfloat16, device=DEV)
+    cache.scatter(0, torch.tensor([[5, 64]], device=DEV), k, k)
+    with pytest.raises(IndexError, match="outside the pool's 64 slots"):
+        pool.check_slot_writes()
+    pool.check_slot_writes()
 
 
 def test_c2_decode_write_is_bit_exact_at_full_pool_size():

@@ -153,6 +153,6 @@ def test_scatter_rejects_null_pointers_before_launching():
     lib = _native.load()
     strides = _native.i64_array([0, 0, 0, 1])
     status = lib.li_kv_scatter(None, None, strides, strides, 1, 1, None, None, None, 16, 16, 8, 2, 8,
-                               _native.LI_BF16, None)
+                               _native.LI_BF16, None, None)
     assert status == _native.LI_EINVAL
     assert "null pointer" in _native.last_error()

@@ -93,6 +93,20 @@ def test_pools_laid_out_differently_are_refused():
                      b.groups)
 
 
+def test_pools_of_2_pow_31_slots_are_refused():
+    """The attention kernels hold slot indices in 32 bits; a bigger pool is refused, not wrapped."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    b = PagedBatch([4])
+    huge_k = b.key_pool[:1].expand(1 << 31, *b.key_pool.shape[1:])
+    huge_v = b.value_pool[:1].expand(1 << 31, *b.value_pool.shape[1:])
+    with pytest.raises(ValueError, match="fewer than 2\\*\\*31 slots"):
+        paged_decode(b.query, huge_k, huge_v, b.slot_table, b.context_lens_t, b.scaling, b.groups)
+    qsl = torch.tensor([0, 1], dtype=torch.int32, device=b.query.device)
+    with pytest.raises(ValueError, match="fewer than 2\\*\\*31 slots"):
+        paged_prefill(b.query, huge_k, huge_v, b.slot_table, b.context_lens_t, qsl, 1, b.scaling, b.groups)
+
+
 def test_fewer_than_one_split_is_refused():
     b = PagedBatch([4])
     with pytest.raises(ValueError, match="num_splits must be >= 1"):

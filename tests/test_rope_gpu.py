@@ -104,7 +104,9 @@ def test_out_of_range_slots_are_skipped_and_others_untouched():
     slots = torch.tensor([[3, -1, 32, 7]], device=DEV)
     before_k, before_v = kp.clone(), vp.clone()
     q_embed, k_embed = apply_rotary_pos_emb(q, k, cos, sin)
-    got_q = rope_kv_write(q, k, v, cos, sin, slots, kp, vp)
+    bad = torch.zeros(1, dtype=torch.int32, device=DEV)
+    got_q = rope_kv_write(q, k, v, cos, sin, slots, kp, vp, bad_slots=bad)
+    assert int(bad.item()) == 2  # one count per token, not per head or element
     np.testing.assert_array_equal(_bits(got_q), _bits(q_embed))
     rows_k, rows_v = tokens_first(k_embed), tokens_first(v)
     for i, s in ((0, 3), (3, 7)):
