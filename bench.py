@@ -131,6 +131,67 @@ def _time_prefill(step, steps, warmup):
     return [a.elapsed_time(b) for a, b in marks]
 
 
+def graph_replay_us(fn, replays: int = 100, repeats: int = 5) -> float:
+    """Per-replay microseconds of `fn` captured once into a HIP graph.
+
+    `replays` back-to-back replays are bracketed by HIP events; the best of
+    `repeats` such runs is kept (the reference's own method for its layer
+    timings). Host launch cost is out of the figure.
+    """
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(repeats):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(replays):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / replays)
+    del graph
+    return best
+
+
+def _decode_call(step):
+    kv = PagedKV(step.key_pool, step.value_pool, step.slot_table, step.context_lens)
+    q = step.query.unsqueeze(2)
+    geo = step.geometry
+    return lambda: paged_attention(q, kv, geo.scaling, geo.groups)
+
+
+def _prefill_call(step):
+    geo = step.geometry
+    kv = PagedKV(step.key_pool, step.value_pool, step.slot_table, step.context_lens,
+                 query_start_loc=step.query_start_loc, max_query_len=step.max_query_len,
+                 host_context_lens=tuple(step.host_context_lens), host_query_lens=tuple(step.host_query_lens))
+    q = step.query.transpose(0, 1).unsqueeze(0)
+    return lambda: paged_attention(q, kv, geo.scaling, geo.groups)
+
+
+def _graph_hbm(entry: dict, fn, nbytes: int) -> dict:
+    us = graph_replay_us(fn)
+    entry["graph_replay_us"] = round(us, 2)
+    entry["graph_replay_frac_hbm"] = round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    return entry
+
+
+def _graph_mfma(entry: dict, fn, flops: int) -> dict:
+    us = graph_replay_us(fn)
+    entry["graph_replay_us"] = round(us, 2)
+    entry["graph_replay_frac_bf16_peak"] = round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)
+    return entry
+
+
 def _time_rope(batch, tokens, geo, iters=50, num_slots=1 << 20, seed=0):
     """Fused RoPE + slot-write vs the reference's separate torch ops (rotary, permute, index_put_)."""
     from liteinfer_amd.rope import apply_rotary_pos_emb, rope_kv_write
@@ -208,51 +269,123 @@ def _time_rope(batch, tokens, geo, iters=50, num_slots=1 << 20, seed=0):
     }
 
 
-def cpu_baseline(step, max_seconds: float = 20.0) -> dict:
-    """Dense eager attention (fp32, torch CPU threads) over the first sequences of the step."""
-    from oracle import baseline
-
-    cores = min(len(os.sched_getaffinity(0)), 16)
-    torch.set_num_threads(cores)
-    geo = step.geometry
-    n = 8
-    ctxs = step.host_context_lens[:n]
-    width = max(ctxs)
-    table = step.slot_table[:n, :width]
-    uniq, inverse = torch.unique(table, return_inverse=True)
-    kp = step.key_pool[uniq].float().cpu()
-    vp = step.value_pool[uniq].float().cpu()
-    q = step.query[:n].float().cpu()
-    local = inverse.cpu()
-    ctx_t = torch.tensor(ctxs)
-    baseline.decode("eager", q, kp, vp, local, ctx_t, geo.scaling, geo.groups)  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 5 and time.perf_counter() - t_start < max_seconds:
-        t0 = time.perf_counter()
-        baseline.decode("eager", q, kp, vp, local, ctx_t, geo.scaling, geo.groups)
-        times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
-    t0 = time.perf_counter()
-    baseline.decode("sdpa", q, kp, vp, local, ctx_t, geo.scaling, geo.groups)
-    sdpa_sec = time.perf_counter() - t0
-    nbytes = decode_bytes(ctxs, geo)
-    cpu_model = ""
+def _cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
             if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
+                return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return "unknown"
+
+
+def _median_of(fn, calls: int = 5) -> float:
+    """Median wall seconds of `calls` calls after one untimed warm-up."""
+    fn()
+    times = []
+    for _ in range(calls):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def _host_rows(step, rows: int, width: int):
+    """The fp32 host copy of the pool rows the first `rows` sequences read, and their local table."""
+    table = step.slot_table[:rows, :width]
+    uniq, inverse = torch.unique(table, return_inverse=True)
+    return step.key_pool[uniq].float().cpu(), step.value_pool[uniq].float().cpu(), inverse.cpu()
+
+
+def _cpu_decode(step, budget_s: float) -> dict:
+    """eager and sdpa medians over as many of the step's sequences as fit the time budget."""
+    from oracle import baseline
+
+    geo = step.geometry
+    n = step.batch
+    while True:
+        ctxs = step.host_context_lens[:n]
+        kp, vp, local = _host_rows(step, n, max(ctxs))
+        q = step.query[:n].float().cpu()
+        ctx_t = torch.tensor(ctxs)
+        run = lambda kind: baseline.decode(kind, q, kp, vp, local, ctx_t, geo.scaling, geo.groups)
+        t0 = time.perf_counter()
+        run("eager")
+        first = time.perf_counter() - t0
+        # 6 eager + 6 sdpa calls follow; halve the sample until they fit.
+        if n == 1 or 12 * first <= budget_s:
+            break
+        n = max(1, n // 2)
+        del kp, vp, local, q
+    eager = _median_of(lambda: run("eager"))
+    sdpa = _median_of(lambda: run("sdpa"))
+    nbytes = decode_bytes(ctxs, geo)
     return {
-        "value": round(nbytes / sec / 1e9, 3),
+        "sequences": f"{n} of {step.batch}",
+        "context_tokens": sum(ctxs),
+        "eager_ms": round(eager * 1e3, 2),
+        "sdpa_ms": round(sdpa * 1e3, 2),
+        "eager_GB/s": round(nbytes / eager / 1e9, 3),
+        "sdpa_GB/s": round(nbytes / sdpa / 1e9, 3),
+    }
+
+
+def _cpu_packed(step, budget_s: float) -> dict:
+    """eager and sdpa medians over config 3's whole packed pass (sequence by sequence, as the reference)."""
+    from oracle import baseline
+
+    geo = step.geometry
+    kp, vp, local = _host_rows(step, len(step.host_query_lens), step.slot_table.shape[1])
+    q = step.query.float().cpu()
+    ctx_t = step.context_lens.cpu()
+    qlens = list(step.host_query_lens)
+    run = lambda kind: baseline.packed(kind, q, kp, vp, local, ctx_t, qlens, geo.scaling, geo.groups)
+    eager = _median_of(lambda: run("eager"))
+    sdpa = _median_of(lambda: run("sdpa"))
+    flops = prefill_flops(step.host_query_lens, step.host_context_lens, geo)
+    return {
+        "sequences": f"all {len(qlens)} (8 chunks + 56 one-query rows)",
+        "query_tokens": sum(qlens),
+        "eager_ms": round(eager * 1e3, 2),
+        "sdpa_ms": round(sdpa * 1e3, 2),
+        "eager_TFLOP/s": round(flops / eager / 1e12, 4),
+        "sdpa_TFLOP/s": round(flops / sdpa / 1e12, 4),
+    }
+
+
+def cpu_baseline(seed: int = 0, device: str = "cuda", budget_s: float = 20.0, gpu_ms: dict | None = None) -> dict:
+    """The reference's dense eager and sdpa attention (fp32 torch, every host core) per config.
+
+    Config 2 and 4 decode steps (all sequences, or the largest halving of the
+    batch whose 12 calls fit `budget_s`) and config 3's packed pass; each the
+    median of 5 calls after a warm-up. `value` is config 2's eager rate.
+    """
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    configs = {}
+    step = decode_step("c2", seed=seed, device=device)
+    configs["c2"] = _cpu_decode(step, budget_s)
+    del step
+    step = packed_step("c3", seed=seed, device=device)
+    configs["c3"] = _cpu_packed(step, budget_s)
+    del step
+    step = decode_step("c4", seed=seed, device=device)
+    configs["c4"] = _cpu_decode(step, budget_s)
+    del step
+    for name, ms in (gpu_ms or {}).items():
+        if name in configs:
+            configs[name]["gpu_paged_ms_full_config"] = ms
+    c2 = configs["c2"]
+    return {
+        "value": c2["eager_GB/s"],
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"dense eager attention (oracle/baseline.py, fp32 torch) over the first {n} of config 2's 64 "
-                   f"sequences ({sum(ctxs)} context tokens), median of {len(times)} calls = {sec * 1e3:.1f} ms; "
-                   f"sdpa one call = {sdpa_sec * 1e3:.1f} ms ({nbytes / sdpa_sec / 1e9:.3f} GB/s); CPU: {cpu_model}"),
+        "cpu_model": _cpu_model(),
+        "sample": (f"dense eager attention (oracle/baseline.py, fp32 torch on {cores} threads) over config 2's "
+                   f"decode step, {c2['sequences']} sequences ({c2['context_tokens']} context tokens): median of "
+                   f"5 calls = {c2['eager_ms']} ms; sdpa {c2['sdpa_ms']} ms; configs 3 and 4 in `configs`"),
+        "configs": configs,
     }
 
 
@@ -327,6 +460,7 @@ def main() -> int:
     value = (d_bytes + s_bytes) / (ms_per_step * 1e-3) / 1e9
     decode_avg_ms = statistics.mean(decode_ms)
     achieved = d_bytes / (decode_avg_ms * 1e-3) / 1e9
+    decode_graph_us = graph_replay_us(_decode_call(step))
 
     result = {
         "metric": METRIC,
@@ -363,6 +497,12 @@ def main() -> int:
             "traffic": _traffic(),
             "algorithmic_bytes_per_launch": d_bytes,
             "avg_launch_us": round(decode_avg_ms * 1e3, 2),
+            "graph_replay": {
+                "avg_launch_us": round(decode_graph_us, 2),
+                "achieved": round(d_bytes / (decode_graph_us * 1e-6) / 1e9, 1),
+                "frac": round(d_bytes / (decode_graph_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "method": "one decode call captured in a HIP graph; 100 replays between HIP events, best of 5",
+            },
         },
     }
 
@@ -380,6 +520,7 @@ def main() -> int:
             "frac_hbm": round(c4_bytes / (c4_avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "context_tokens": sum(c4.host_context_lens),
         }
+        _graph_hbm(secondary["decode_c4"], _decode_call(c4), c4_bytes)
         # The same decode steps over an fp8 (e4m3) pool: half the K/V bytes.
         c4 = to_fp8_pool(c4)
         _, c4_ms8 = _time_decode(c4, max(10, args.steps // 4), 3)
@@ -391,6 +532,7 @@ def main() -> int:
             "frac_hbm": round(c4_bytes8 / (c4_avg8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "speedup_vs_bf16_kv": round(c4_avg / c4_avg8, 3),
         }
+        _graph_hbm(secondary["decode_c4_fp8_kv"], _decode_call(c4), c4_bytes8)
         del c4
         torch.cuda.empty_cache()
         c2 = to_fp8_pool(decode_step("c2", seed=args.seed))
@@ -403,6 +545,7 @@ def main() -> int:
             "frac_hbm": round(c2_bytes8 / (c2_avg8 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "speedup_vs_bf16_kv": round(decode_avg_ms / c2_avg8, 3),
         }
+        _graph_hbm(secondary["decode_c2_fp8_kv"], _decode_call(c2), c2_bytes8)
         del c2
         torch.cuda.empty_cache()
         c3 = packed_step("c3", seed=args.seed)
@@ -416,6 +559,7 @@ def main() -> int:
             "visible_pair_flops": flops,
             "query_tokens": sum(c3.host_query_lens),
         }
+        _graph_mfma(secondary["prefill_c3"], _prefill_call(c3), flops)
         geo3, c3_tokens = c3.geometry, sum(c3.host_query_lens)
         c3 = to_fp8_pool(c3)
         c3_avg8 = statistics.mean(_time_prefill(c3, max(10, args.steps // 4), 3))
@@ -424,6 +568,7 @@ def main() -> int:
             "TFLOP/s": round(flops / (c3_avg8 * 1e-3) / 1e12, 2),
             "frac_bf16_peak": round(flops / (c3_avg8 * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         }
+        _graph_mfma(secondary["prefill_c3_fp8_kv"], _prefill_call(c3), flops)
         del c3
         torch.cuda.empty_cache()
         # Config 3's two kinds of work on their own: the 8 chunks (MFMA-bound)
@@ -437,6 +582,7 @@ def main() -> int:
             "TFLOP/s": round(part_flops / (part_avg * 1e-3) / 1e12, 2),
             "frac_bf16_peak": round(part_flops / (part_avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         }
+        _graph_mfma(secondary["prefill_c3_chunks"], _prefill_call(part), part_flops)
         del part
         torch.cuda.empty_cache()
         part = packed_step("custom", seed=args.seed, chunks=[], decode_contexts=rows)
@@ -447,6 +593,7 @@ def main() -> int:
             "GB/s": round(part_bytes / (part_avg * 1e-3) / 1e9, 1),
             "frac_hbm": round(part_bytes / (part_avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         }
+        _graph_hbm(secondary["c3_decode_rows"], _prefill_call(part), part_bytes)
         del part
         torch.cuda.empty_cache()
         # Long chunks: 8 chunks of 2048 queries over 8192 cached keys.
@@ -458,6 +605,7 @@ def main() -> int:
             "TFLOP/s": round(part_flops / (part_avg * 1e-3) / 1e12, 2),
             "frac_bf16_peak": round(part_flops / (part_avg * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
         }
+        _graph_mfma(secondary["prefill_8x2048_over_8192"], _prefill_call(part), part_flops)
         del part
         torch.cuda.empty_cache()
         secondary["rope_kv_write_c3"] = _time_rope(1, c3_tokens, geo3)
@@ -475,8 +623,11 @@ def main() -> int:
         torch.cuda.empty_cache()
 
     if not args.no_cpu_baseline:
-        sample_step = decode_step("c2", seed=args.seed)
-        result["cpu_baseline"] = cpu_baseline(sample_step)
+        gpu_ms = {"c2": round(result["roofline"]["avg_launch_us"] / 1e3, 4)}
+        for name, key in (("c3", "prefill_c3"), ("c4", "decode_c4")):
+            if key in result.get("secondary", {}):
+                gpu_ms[name] = round(result["secondary"][key]["avg_us"] / 1e3, 4)
+        result["cpu_baseline"] = cpu_baseline(args.seed, gpu_ms=gpu_ms)
 
     print(json.dumps(result))
     return 0
