@@ -52,6 +52,9 @@ METRIC = "paged-decode HBM GB/s (% of peak); prefill attn TFLOP/s; e2e output to
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = ROOT / "profiles" / "decode_c2_traffic.json"
+# Untimed calls before each secondary workload's timed ones: enough for the
+# clocks to settle after the previous workload (a few ms of work).
+SECONDARY_WARMUP = 20
 
 
 def decode_bytes(ctxs, geo, elem=2, kv_elem=None) -> int:
@@ -511,7 +514,7 @@ def main() -> int:
         del step
         torch.cuda.empty_cache()
         c4 = decode_step("c4", seed=args.seed)
-        _, c4_ms = _time_decode(c4, max(10, args.steps // 4), 3)
+        _, c4_ms = _time_decode(c4, max(10, args.steps // 4), SECONDARY_WARMUP)
         c4_bytes = decode_bytes(c4.host_context_lens, c4.geometry)
         c4_avg = statistics.mean(c4_ms)
         secondary["decode_c4"] = {
@@ -523,7 +526,7 @@ def main() -> int:
         _graph_hbm(secondary["decode_c4"], _decode_call(c4), c4_bytes)
         # The same decode steps over an fp8 (e4m3) pool: half the K/V bytes.
         c4 = to_fp8_pool(c4)
-        _, c4_ms8 = _time_decode(c4, max(10, args.steps // 4), 3)
+        _, c4_ms8 = _time_decode(c4, max(10, args.steps // 4), SECONDARY_WARMUP)
         c4_bytes8 = decode_bytes(c4.host_context_lens, c4.geometry, kv_elem=1)
         c4_avg8 = statistics.mean(c4_ms8)
         secondary["decode_c4_fp8_kv"] = {
@@ -536,7 +539,7 @@ def main() -> int:
         del c4
         torch.cuda.empty_cache()
         c2 = to_fp8_pool(decode_step("c2", seed=args.seed))
-        _, c2_ms8 = _time_decode(c2, max(10, args.steps // 4), 3)
+        _, c2_ms8 = _time_decode(c2, max(10, args.steps // 4), SECONDARY_WARMUP)
         c2_bytes8 = decode_bytes(c2.host_context_lens, c2.geometry, kv_elem=1)
         c2_avg8 = statistics.mean(c2_ms8)
         secondary["decode_c2_fp8_kv"] = {
@@ -549,7 +552,7 @@ def main() -> int:
         del c2
         torch.cuda.empty_cache()
         c3 = packed_step("c3", seed=args.seed)
-        c3_ms = _time_prefill(c3, max(10, args.steps // 4), 3)
+        c3_ms = _time_prefill(c3, max(10, args.steps // 4), SECONDARY_WARMUP)
         c3_avg = statistics.mean(c3_ms)
         flops = prefill_flops(c3.host_query_lens, c3.host_context_lens, c3.geometry)
         secondary["prefill_c3"] = {
@@ -562,7 +565,7 @@ def main() -> int:
         _graph_mfma(secondary["prefill_c3"], _prefill_call(c3), flops)
         geo3, c3_tokens = c3.geometry, sum(c3.host_query_lens)
         c3 = to_fp8_pool(c3)
-        c3_avg8 = statistics.mean(_time_prefill(c3, max(10, args.steps // 4), 3))
+        c3_avg8 = statistics.mean(_time_prefill(c3, max(10, args.steps // 4), SECONDARY_WARMUP))
         secondary["prefill_c3_fp8_kv"] = {
             "avg_us": round(c3_avg8 * 1e3, 2),
             "TFLOP/s": round(flops / (c3_avg8 * 1e-3) / 1e12, 2),
@@ -575,7 +578,7 @@ def main() -> int:
         # and the 56 one-query rows (HBM-bound), each as a packed pass.
         chunks, rows = c3_shapes(args.seed)
         part = packed_step("custom", seed=args.seed, chunks=chunks, decode_contexts=[])
-        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 4), 3))
+        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 4), SECONDARY_WARMUP))
         part_flops = prefill_flops(part.host_query_lens, part.host_context_lens, part.geometry)
         secondary["prefill_c3_chunks"] = {
             "avg_us": round(part_avg * 1e3, 2),
@@ -586,7 +589,7 @@ def main() -> int:
         del part
         torch.cuda.empty_cache()
         part = packed_step("custom", seed=args.seed, chunks=[], decode_contexts=rows)
-        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 4), 3))
+        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 4), SECONDARY_WARMUP))
         part_bytes = decode_bytes(part.host_context_lens, part.geometry)
         secondary["c3_decode_rows"] = {
             "avg_us": round(part_avg * 1e3, 2),
@@ -598,7 +601,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         # Long chunks: 8 chunks of 2048 queries over 8192 cached keys.
         part = packed_step("custom", seed=args.seed, chunks=[(2048, 8192)] * 8, decode_contexts=[])
-        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 20), 2))
+        part_avg = statistics.mean(_time_prefill(part, max(10, args.steps // 20), 5))
         part_flops = prefill_flops(part.host_query_lens, part.host_context_lens, part.geometry)
         secondary["prefill_8x2048_over_8192"] = {
             "avg_us": round(part_avg * 1e3, 2),

@@ -184,12 +184,12 @@ def _paged_decode_step(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_
     return out.unsqueeze(2)
 
 
-# Rates the choice below uses (measured on MI355X): the decode kernel streams
-# K/V at about 6 TB/s, the prefill kernel folds about 1 PFLOP/s of visible
-# pairs. The prefill kernel folds a one-query sequence's whole context in one
-# work-group, so it takes them only when contexts are bounded.
-_DECODE_BYTES_PER_S = 6e12
-_PREFILL_FLOPS_PER_S = 1e15
+# MI355X (gfx950) published peaks. Only their ratio matters to the choice
+# below: it compares the roofline times of two kinds of work on one device.
+_HBM_PEAK_BYTES_PER_S = 8.0e12
+_MFMA_PEAK_FLOPS_PER_S = 2.5e15
+# The prefill kernel folds a one-query sequence's whole context into one
+# work-group, so it takes such rows only while contexts are bounded.
 _LONGEST_ROW_FOR_PREFILL = 8192
 
 
@@ -198,25 +198,29 @@ def _one_query_rows_to_decode_kernel(query_lens, context_lens, num_heads: int, n
     """Whether a packed pass's one-query sequences should go to the decode kernel.
 
     False (the prefill kernel serves them beside the chunks, in one launch)
-    when there are none, or when streaming their keys takes less than half
-    the time the chunks' MFMA work does and no context is longer than
-    ``_LONGEST_ROW_FOR_PREFILL``: their loads then fill in behind the chunks'
-    units (config 3: 430-441 -> 420 us). Otherwise, and always on fp8 pools,
-    the decode kernel's split over the whole grid serves them (a
-    decode-heavy pass: 644 -> 629 us).
-    The answer is the same either way.
+    when there are none, or when streaming their keys has a roofline time
+    (bytes at peak HBM bandwidth) no longer than the chunks' (flops at peak
+    MFMA rate) and no context is longer than ``_LONGEST_ROW_FOR_PREFILL``:
+    the rows' loads then overlap the chunks' matrix work and fill the tail of
+    the persistent queue, where they are queued after the chunk blocks
+    (config 3: rows 0.55x the chunks' roofline time; in-kernel 72 us for rows
+    that take 99 us in their own launch). Once the rows' memory time passes
+    the chunks' matrix time there is nothing left to hide them behind, and
+    the decode kernel's split over the whole grid streams them faster. On fp8
+    pools every prefill stage also converts in LDS, which folded rows would
+    pay too, so they always go to the decode kernel. The answer is the same
+    attention either way; the rule depends on no box-specific rate, only on
+    the ratio of the two peaks.
     """
     rows = [c for q, c in zip(query_lens, context_lens) if q == 1]
     if not rows:
         return False
     if pool_element_size < 2 or max(rows) > _LONGEST_ROW_FOR_PREFILL:
-        # fp8 pools: every prefill stage also converts in LDS, which the
-        # one-query rows' stages pay too (config 3: 394 -> 404 us in-kernel).
         return True
     row_bytes = sum(rows) * num_kv_heads * head_dim * pool_element_size * 2
     chunk_flops = sum(4 * num_heads * head_dim * (q * (c - q) + q * (q + 1) / 2)
                       for q, c in zip(query_lens, context_lens) if q > 1)
-    return row_bytes / _DECODE_BYTES_PER_S > 0.5 * chunk_flops / _PREFILL_FLOPS_PER_S
+    return row_bytes / _HBM_PEAK_BYTES_PER_S > chunk_flops / _MFMA_PEAK_FLOPS_PER_S
 
 
 def _paged_packed(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_groups: int) -> torch.Tensor:
