@@ -27,28 +27,14 @@ constexpr int kMinTilesToSplit = 4;
 constexpr int kMaxPartitions = 1024;
 constexpr int kDefaultBlockKv = 64;
 
-int env_int(const char* name, int fallback) {
-  const char* v = std::getenv(name);
-  if (!v || !*v) return fallback;
-  const int x = std::atoi(v);
-  return x > 0 ? x : fallback;
-}
-
-// A 0/1 switch from the environment; unset or empty gives `fallback`.
-bool env_flag(const char* name, bool fallback) {
-  const char* v = std::getenv(name);
-  if (!v || !*v) return fallback;
-  return std::atoi(v) != 0;
-}
-
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 // Returns the partition count of the grid and the fixed partition length
 // (0 when the whole context is one partition).
 void decode_policy(int batch, int num_kv_heads, int max_context, int num_cus, int block_kv,
                    int* parts, int* plen) {
-  static const int target = env_int("LI_DECODE_WAVES_PER_CU", kTargetWavesPerCu);
-  static const int max_part = env_int("LI_DECODE_MAX_PARTITION", kMaxPartition);
+  const int target = kTargetWavesPerCu;
+  const int max_part = kMaxPartition;
   const int tile = block_kv > 0 ? block_kv : kDefaultBlockKv;
   *parts = 1;
   *plen = 0;
@@ -84,31 +70,22 @@ constexpr int kBalancedWavesPerCu = 4;
 constexpr int kSegmentCost = 2;
 
 int balanced_waves(int num_cus) {
-  static const int per_cu = env_int("LI_DECODE_BALANCED_WAVES_PER_CU", kBalancedWavesPerCu);
-  return std::max(1, num_cus) * per_cu;
+  return std::max(1, num_cus) * kBalancedWavesPerCu;
 }
 
 // KV heads per partial slot of the balanced split: kDecodeHeadGroup when
 // the head-grouped kernel serves the shape (a 16-bit pool, num_kv_heads a
 // multiple of the group), else one. Grouping pays on 16-bit pools (config 2:
 // 204 -> 196 us) and costs on fp8 ones (config 4: 191 -> 200 us), whose
-// per-head rows are already half as long. LI_DECODE_GROUPED=0 switches it off.
+// per-head rows are already half as long.
 int balanced_part_heads(int num_kv_heads, bool kv_fp8) {
-  static const bool grouped = env_flag("LI_DECODE_GROUPED", true);
-  return grouped && !kv_fp8 && num_kv_heads % kDecodeHeadGroup == 0 ? kDecodeHeadGroup : 1;
+  return !kv_fp8 && num_kv_heads % kDecodeHeadGroup == 0 ? kDecodeHeadGroup : 1;
 }
 
 // What starting a segment (its query, its slots, the ring's first tile)
 // costs the head-grouped decode, in 32-key tiles: the balanced split charges
 // it so that waves meeting many short contexts take fewer tiles.
-// LI_DECODE_SEGMENT_COST overrides it (0 and up).
-int segment_cost() {
-  static const int cost = [] {
-    const char* v = std::getenv("LI_DECODE_SEGMENT_COST");
-    return (v && *v) ? std::max(0, std::atoi(v)) : kSegmentCost;
-  }();
-  return cost;
-}
+int segment_cost() { return kSegmentCost; }
 
 size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads) {
   // Sized for either pool type (the plan calls do not know it).
