@@ -402,9 +402,11 @@ def _traffic():
 
 
 def _only_prefill(workload: str, seed: int, steps: int, warmup: int) -> int:
-    """One packed prefill workload alone: config 3, its 8 chunks, or 8 chunks of 2048 over 8192."""
+    """One packed prefill workload alone: config 3 (bf16 or fp8 pool), its 8 chunks, or 8 chunks of 2048 over 8192."""
     if workload == "c3":
         step = packed_step("c3", seed=seed)
+    elif workload == "c3_fp8":
+        step = to_fp8_pool(packed_step("c3", seed=seed))
     elif workload == "c3_chunks":
         chunks, _ = c3_shapes(seed)
         step = packed_step("custom", seed=seed, chunks=chunks, decode_contexts=[])
@@ -430,7 +432,7 @@ def main() -> int:
     parser.add_argument("--copy-calibration", action="store_true",
                         help="first run three 1 GiB device-to-device copies (a reference kernel of known "
                              "size for rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
-    parser.add_argument("--only-prefill", choices=["c3", "c3_chunks", "long"],
+    parser.add_argument("--only-prefill", choices=["c3", "c3_fp8", "c3_chunks", "long"],
                         help="time only this packed prefill pass (for profiling) and print its line")
     args = parser.parse_args()
 

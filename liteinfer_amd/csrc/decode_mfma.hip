@@ -38,6 +38,10 @@
 
 #include <cstdlib>
 
+#ifndef LI_DEC_STREAM
+#define LI_DEC_STREAM true
+#endif
+
 namespace li {
 namespace {
 
@@ -71,8 +75,8 @@ __device__ __forceinline__ void issue_tile(char* stage, const char* __restrict__
     const int key = rr * L::kInsts + i;
     const uint32_t dst = lds_addr(stage + i * 1024);  // rows kRowsPerInst * i ..: 1 KiB per instruction
     // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
-    dma16(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), (uint32_t)keys[i], row_bytes), dst);
-    dma16(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), (uint32_t)keys[i], row_bytes), dst + 32 * L::kRowBytes);
+    dma16<LI_DEC_STREAM>(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), (uint32_t)keys[i], row_bytes), dst);
+    dma16<LI_DEC_STREAM>(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), (uint32_t)keys[i], row_bytes), dst + 32 * L::kRowBytes);
   }
 }
 

@@ -136,16 +136,30 @@ __device__ __forceinline__ Frag lds_read_f8_vt(uint32_t addr) {
 // LDS read, which would serialise the two stages. Here the kernel counts the
 // loads itself (li_wait_vm below) and the "memory" clobbers keep every other
 // memory access in program order around them.
+// kStream: the rows are read once (non-temporal hint); otherwise they stay
+// in L2 for the other work-groups that read them.
+template <bool kStream = true>
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "global_load_lds_dwordx4 %2, off nt\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
-      : "memory");
+  if constexpr (kStream) {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
+        : "memory");
+  } else {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(g)
+        : "memory");
+  }
 }
 
 // A work-group barrier that orders LDS only: this wave's LDS operations are

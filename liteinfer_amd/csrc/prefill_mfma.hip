@@ -63,6 +63,16 @@ constexpr int kStageKeys = 64;
 #ifndef LI_PREFILL_PIPE
 #define LI_PREFILL_PIPE 1
 #endif
+// The prefill's K/V loads keep their lines in L2 (no non-temporal hint):
+// the other query blocks of a sequence, folded at about the same time on
+// the same XCD, read the same rows (config 3's chunks: 338 -> 318 us, 8
+// chunks of 2048 over 8192 keys: 2065 -> 1947 us). Choosing the hint per
+// unit (streaming the single-block sequences) measured slower: the branch
+// costs more scalar registers than the hint saves.
+__device__ __forceinline__ void dma16_kv(const char* k, const char* v, uint32_t kdst, uint32_t vdst) {
+  dma16<false>(k, kdst);
+  dma16<false>(v, vdst);
+}
 
 // Issues this wave's share of the direct-to-LDS loads of the 64 keys whose
 // first key is entry `t` of the staged slots. The stage takes 2 * kInsts
@@ -90,8 +100,8 @@ __device__ __forceinline__ void issue_stage(uint32_t stage, const char* __restri
     const int key = rr * L::kInsts + i;
     const uint32_t dst = stage + half * L::kTileBytes + i * 1024;
     // Lane nn writes slot nn of its row: global chunk nn ^ swizzle(key).
-    dma16(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), slot[ii], row_bytes), dst);
-    dma16(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), dst + 32 * L::kRowBytes);
+    dma16_kv(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), slot[ii], row_bytes),
+             row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), dst, dst + 32 * L::kRowBytes);
   }
 }
 
@@ -168,10 +178,13 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   const int first_tok = a.qsl[seq];
   const int nq = a.qsl[seq + 1] - first_tok;
   const int bq = a.block_q;  // query tokens per block = 32 W / groups
-  const int q0 = qblock * bq;
-  if (q0 >= nq) continue;
+  // Blocks are cut from the end of the chunk: block nblk - 1 ends at its
+  // last query and only block 0 (the one with the fewest keys) is partial.
+  const int nblk = (nq + bq - 1) / bq;
+  if (qblock >= nblk) continue;
+  const int q1 = nq - (nblk - 1 - qblock) * bq;
+  const int q0 = max(q1 - bq, 0);
   if (nq == 1 && a.single_query_elsewhere) continue;  // the decode kernel serves it
-  const int q1 = min(q0 + bq, nq);
   const int ctx = a.ctx[seq];
   const int pos0 = ctx - nq;   // position of the sequence's first query
   const int kend = pos0 + q1;  // keys this block reads: [0, kend)
@@ -186,7 +199,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   for (int nb = 0; nb < 2; ++nb) {
     const int row = 32 * w + 16 * nb + n;
     const int ql = row / G;
-    real[nb] = row < bq * G && q0 + ql < nq;
+    real[nb] = row < bq * G && q0 + ql < q1;
     pos[nb] = real[nb] ? pos0 + q0 + ql : kend;
     tok[nb] = first_tok + q0 + ql;
     head[nb] = kvh * G + row % G;
@@ -452,27 +465,35 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
 // region and the V rows in another (kdst / vdst: this stage's 32-key tiles
 // of K, of V, 32 rows apart), so that the per-lane read addresses of either
 // region plus every buffer's constant offset fit a DS instruction's 16-bit
-// immediate.
+// immediate. Split in two so the slot reads can go out well before the loads
+// that need them: stage_slot_reads reads the kPer slots this wave loads
+// (entry `t` first), stage_fire issues the loads of K and V rows.
 template <typename L, int W>
-__device__ __forceinline__ void issue_stage_split(uint32_t kdst, uint32_t vdst, const char* __restrict__ kpool,
-                                                  const char* __restrict__ vpool, const int* __restrict__ sl,
-                                                  uint32_t row_bytes, int t, int lane, int w) {
+__device__ __forceinline__ void stage_slot_reads(uint32_t (&slot)[2 * L::kInsts / W], const int* __restrict__ sl,
+                                                 int t, int lane, int w) {
   constexpr int kPer = 2 * L::kInsts / W;
   static_assert(kPer >= 1 && kPer * W == 2 * L::kInsts, "waves must split the stage's loads evenly");
-  const int rr = lane / L::kCh, nn = lane % L::kCh;
-  uint32_t slot[kPer];
+  const int rr = lane / L::kCh;
 #pragma unroll
   for (int ii = 0; ii < kPer; ++ii) {
     const int p = w * kPer + ii, half = p / L::kInsts, i = p % L::kInsts;
     slot[ii] = (uint32_t)sl[t + 32 * half + rr * L::kInsts + i];
   }
+}
+
+template <typename L, int W>
+__device__ __forceinline__ void stage_fire(uint32_t kdst, uint32_t vdst, const char* __restrict__ kpool,
+                                           const char* __restrict__ vpool, const uint32_t (&slot)[2 * L::kInsts / W],
+                                           uint32_t row_bytes, int lane, int w) {
+  constexpr int kPer = 2 * L::kInsts / W;
+  const int rr = lane / L::kCh, nn = lane % L::kCh;
 #pragma unroll
   for (int ii = 0; ii < kPer; ++ii) {
     const int p = w * kPer + ii, half = p / L::kInsts, i = p % L::kInsts;
     const int key = rr * L::kInsts + i;
     const uint32_t off = half * 32 * L::kRowBytes + i * 1024;
-    dma16(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), slot[ii], row_bytes), kdst + off);
-    dma16(row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), vdst + off);
+    dma16_kv(row_ptr(kpool + 16 * (nn ^ L::kswizzle(key)), slot[ii], row_bytes),
+             row_ptr(vpool + 16 * (nn ^ L::vswizzle(key)), slot[ii], row_bytes), kdst + off, vdst + off);
   }
 }
 
@@ -596,10 +617,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int first_tok = __builtin_amdgcn_readfirstlane(a.qsl[seq]);
   const int nq = __builtin_amdgcn_readfirstlane(a.qsl[seq + 1]) - first_tok;
   const int bq = a.block_q;
-  const int q0 = qblock * bq;
-  if (q0 >= nq) continue;
+  // Blocks are cut from the end of the chunk: block nblk - 1 ends at its
+  // last query and only block 0 (the one with the fewest keys) is partial.
+  const int nblk = (nq + bq - 1) / bq;
+  if (qblock >= nblk) continue;
+  const int q1 = nq - (nblk - 1 - qblock) * bq;
+  const int q0 = max(q1 - bq, 0);
   if (nq == 1 && a.single_query_elsewhere) continue;
-  const int q1 = min(q0 + bq, nq);
   const int ctx = __builtin_amdgcn_readfirstlane(a.ctx[seq]);
   const int pos0 = ctx - nq;
   const int kend = pos0 + q1;
@@ -620,7 +644,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int nb = 0; nb < 2; ++nb) {
     const int row = 32 * w + 16 * nb + n;
     const int ql = row / G;
-    real[nb] = row < bq * G && q0 + ql < nq;
+    real[nb] = row < bq * G && q0 + ql < q1;
     pos[nb] = real[nb] ? pos0 + q0 + ql : kend;
     tok[nb] = first_tok + q0 + ql;
     head[nb] = kvh * G + row % G;
@@ -678,9 +702,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto stage_slots_loaders = [&](int k0, int count) {  // waves 0-3
     for (int i = tid; i < count; i += 256) sl[(k0 + i) % kSlotRing] = (int)srow[min(k0 + i, kend - 1)];
   };
+  using Slots = uint32_t[2 * L::kInsts / W];
+  auto fire = [&](int buf, const Slots& slot) {
+    stage_fire<L, W>(lds_addr(kst[buf]), lds_addr(vst[buf]), kpool, vpool, slot, row_bytes, lane, w);
+  };
   auto issue = [&](int buf, int st) {
-    issue_stage_split<L, W>(lds_addr(kst[buf]), lds_addr(vst[buf]), kpool, vpool, sl, row_bytes,
-                            (st * kStageKeys) % kSlotRing, lane, w);
+    Slots slot;
+    stage_slot_reads<L, W>(slot, sl, (st * kStageKeys) % kSlotRing, lane, w);
+    fire(buf, slot);
   };
 
   floatx4_t s[2][4];  // scores (log2 units) of the stage between its M and V phases
@@ -696,20 +725,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // LDS latency at every fragment).
   constexpr int kVFrags = 2 * kBlk;    // V^T fragments of a stage (two reads each)
   constexpr int kKFrags = 4 * kSteps;  // K fragments of a stage (one read each)
+#ifndef LI_PP_AHEAD
+#define LI_PP_AHEAD 4
+#endif
+  constexpr int kAhead = LI_PP_AHEAD;  // fragments read ahead of the MFMAs that use them
+#ifndef LI_DIAG_NOLDS
+#define LI_DIAG_NOLDS 0
+#endif
   auto read_v = [&](uint32_t vb, Frag (&vf)[2][kBlk]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int blk = 0; blk < kBlk; ++blk) {
         const uint32_t tb = vb + t * kHalf;
-        vf[t][blk] = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + L::kRow16);
+        if (LI_DIAG_NOLDS == 1 || LI_DIAG_NOLDS == 2) vf[t][blk] = qf[t][blk % kSteps];
+        else vf[t][blk] = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + L::kRow16);
       }
   };
   auto read_k = [&](uint32_t kb, Frag (&kf)[4][kSteps]) __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int j = 0; j < kSteps; ++j) kf[b][j] = lds_read_frag<Frag>(koff[j] + kb + (b >> 1) * kHalf + (b & 1) * L::kRow16);
+      for (int j = 0; j < kSteps; ++j) {
+        if (LI_DIAG_NOLDS == 1 || LI_DIAG_NOLDS == 3) kf[b][j] = qf[b & 1][(j + b) % kSteps];
+        else kf[b][j] = lds_read_frag<Frag>(koff[j] + kb + (b >> 1) * kHalf + (b & 1) * L::kRow16);
+      }
   };
   auto pv_mfma = [&](const Frag (&vf)[2][kBlk]) __attribute__((always_inline)) {
 #pragma unroll
@@ -742,20 +782,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     pv_mfma(vf);
     read_k(kb, kf);
     qk_mfma(kf);
-    // Reads of fragment f + 4 go out with the MFMAs of fragment f; the
-    // first K fragments with the last V^T fragments' MFMAs.
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+    // Reads of fragment f + kAhead go out with the MFMAs of fragment f;
+    // the first K fragments with the last V^T fragments' MFMAs.
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kAhead, 0);
 #pragma unroll
     for (int f = 0; f < kVFrags; ++f) {
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      if (f + 4 < kVFrags) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      if (f + kAhead < kVFrags) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       else __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // row sums
 #pragma unroll
     for (int f = 0; f < kKFrags; ++f) {
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      if (f + 4 < kKFrags) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (f + kAhead < kKFrags) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
