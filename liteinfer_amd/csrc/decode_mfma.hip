@@ -537,12 +537,17 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
   if (pos >= total) return;
   const int64_t end = min(pos + share, total);
 
-  // The sequence holding flattened unit `pos`.
+  // Group-major flattening, (group, sequence, unit), as in decode_balanced:
+  // the waves of different groups fold the same slots at about the same time.
+  const int64_t per_group = total / ngroups;
+  int grp = (int)(pos / per_group);
+  const int64_t gpos = pos - (int64_t)grp * per_group;
+  // The sequence holding unit `gpos` of the group.
   int seq = 0;
-  int64_t before = 0;  // flattened units of the sequences before `seq`
+  int64_t before = 0;  // units of the sequences before `seq`
   for (int s0 = 0; s0 < a.batch; s0 += 64) {
     const int sq = s0 + lane;
-    const int64_t c = sq < a.batch ? units_of(sq) * ngroups : 0;
+    const int64_t c = sq < a.batch ? units_of(sq) : 0;
     int64_t incl = c;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -550,7 +555,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
       const int hi = __shfl_up((int)(incl >> 32), off, 64);
       if (lane >= off) incl += ((int64_t)hi << 32) | (uint32_t)lo;
     }
-    const uint64_t hit = __ballot(before + incl > pos);
+    const uint64_t hit = __ballot(before + incl > gpos);
     if (hit) {
       const int first = __ffsll((long long)hit) - 1;
       const int64_t excl = __shfl(incl - c, first, 64);
@@ -571,12 +576,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
   float* part_lse = a.part_lse + (int64_t)w * 2 * HG * G;
   int ctx = decode_keys(a, seq);
   int nu = (ctx + 31) / 32 + R;  // units of each of the sequence's segments
-  int grp, u0;
-  {
-    const int64_t local = pos - before;
-    grp = (int)(local / nu);
-    u0 = (int)(local - (int64_t)grp * nu);
-  }
+  int u0 = (int)(gpos - before);
   bool first_segment = true;
   while (pos < end) {
     // Units [u0, u1) of this segment are this wave's; its tiles are units
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
       if (t_lo == 0 && lane < HG) {
         // This wave holds the context's first key: the waves holding its
         // pieces, for each head of the group.
-        const int64_t seg = before + (int64_t)grp * nu;
+        const int64_t seg = (int64_t)grp * per_group + before;
         a.pieces[(int64_t)seq * a.num_kv_heads + h0 + lane] =
             int4{w, (int)((seg + nu - 1) / share), first_segment ? 0 : 1, 0};
       }
@@ -650,15 +650,18 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
     }
     pos += u1 - u0;
     u0 = 0;
-    if (++grp == ngroups) {
-      grp = 0;
-      before += (int64_t)nu * ngroups;
-      ++seq;
-      while (pos < end && seq < a.batch && decode_keys(a, seq) == 0) ++seq;
+    before += nu;
+    ++seq;
+    while (seq < a.batch && decode_keys(a, seq) == 0) ++seq;
+    if (seq >= a.batch) {
+      if (++grp == ngroups) break;
+      seq = 0;
+      before = 0;
+      while (seq < a.batch && decode_keys(a, seq) == 0) ++seq;
       if (seq >= a.batch) break;
-      ctx = decode_keys(a, seq);
-      nu = (ctx + 31) / 32 + R;
     }
+    ctx = decode_keys(a, seq);
+    nu = (ctx + 31) / 32 + R;
   }
 }
 
