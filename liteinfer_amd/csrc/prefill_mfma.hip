@@ -7,6 +7,11 @@
 // keys up to its own position, the online softmax runs in fp32 and the
 // weights are rounded to the value dtype before they multiply V.
 //
+// Two kernels: prefill_pp (16-bit pools), where the two waves of each SIMD
+// run half a stage apart so that one feeds the matrix core while the other
+// runs its softmax (described above the kernel), and prefill_mfma (fp8
+// pools), where all eight waves fold each stage in lockstep, described here.
+//
 // A unit of work is (sequence, KV head, block of 256 / G query tokens),
 // folded by one work-group of 8 waves (two per SIMD). Its 256 rows are
 // (query token, head) pairs, head fastest, so the G heads that share a KV
@@ -60,9 +65,6 @@ constexpr int kWaves = 8;
 constexpr int kMinRows = 32 * kWaves;  // rows of a work-group
 constexpr int kStageKeys = 64;
 
-#ifndef LI_PREFILL_PIPE
-#define LI_PREFILL_PIPE 1
-#endif
 // The prefill's K/V loads keep their lines in L2 (no non-temporal hint):
 // the other query blocks of a sequence, folded at about the same time on
 // the same XCD, read the same rows (config 3's chunks: 338 -> 318 us, 8
@@ -525,48 +527,9 @@ constexpr int kPpRing = 4;
 constexpr int kSlotRing = 4096;  // staged slot entries (int32)
 constexpr int kSlotHalfStages = kSlotRing / 2 / kStageKeys;
 
-#ifndef LI_PP_PRIO_M
-#define LI_PP_PRIO_M 2
-#endif
-#ifndef LI_PP_SETPRIO
-#define LI_PP_SETPRIO 1
-#endif
-#if LI_PP_SETPRIO
-#define LI_SETPRIO_HI() __builtin_amdgcn_s_setprio(LI_PP_PRIO_M)
-#define LI_SETPRIO_LO() __builtin_amdgcn_s_setprio(0)
-#else
-#define LI_SETPRIO_HI() \
-  do {                  \
-  } while (0)
-#define LI_SETPRIO_LO() \
-  do {                  \
-  } while (0)
-#endif
-
-#ifdef LI_PREFILL_TRACE
-__device__ long long g_pp_trace[8][1024];
-__device__ long long g_pp_units[256][64];  // per work-group: (time << 20 | ns << 1 | end) per unit event
-#define LI_UNIT_TRACE(endflag, nsv)                                                              \
-  do {                                                                                            \
-    if (tid == 0 && blockIdx.x < 256 && ucount < 64)                                              \
-      g_pp_units[blockIdx.x][ucount++] = (__builtin_amdgcn_s_memtime() << 20) | ((nsv) << 1) | (endflag); \
-  } while (0)
-#define LI_TRACE(ev)                                                                              \
-  do {                                                                                            \
-    if (blockIdx.x == 0 && tcount < 1024) {                                                       \
-      const long long t_ = __builtin_amdgcn_s_memtime();                                          \
-      if (lane == 0) g_pp_trace[w][tcount] = (t_ << 4) | (ev);                                    \
-      ++tcount;                                                                                   \
-    }                                                                                             \
-  } while (0)
-#else
-#define LI_TRACE(ev) \
-  do {               \
-  } while (0)
-#define LI_UNIT_TRACE(endflag, nsv) \
-  do {                              \
-  } while (0)
-#endif
+// Wave priority of the matrix phase: an MFMA that waits for issue behind the
+// other wave's vector work leaves the matrix core idle.
+constexpr int kPpMatrixPriority = 2;
 
 template <typename T, int D>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp(AttnArgs a) {
@@ -588,9 +551,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool late = w >= 4;  // waves 4-7 run half a stage behind
-#ifdef LI_PREFILL_TRACE
-  int tcount = 0, ucount = 0;
-#endif
   const int n = lane & 15, g = lane >> 4;
 
   const int nqueues = a.num_kv_heads % kPrefillQueues == 0 ? kPrefillQueues : 1;
@@ -604,7 +564,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int next_unit = 0;  // tid 0: the unit claimed for after this one
   for (;;) {
   lds_barrier();
-  LI_TRACE(5);
   // Values read from memory are made wave-uniform explicitly, so every
   // branch on them below is a scalar branch (no exec-masked code paths).
   const int unit = __builtin_amdgcn_readfirstlane(s_unit);
@@ -633,7 +592,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // atomic's round trip is hidden, yet late enough that a work-group that
   // finishes early still takes the heaviest unit left.
   const int claim_at = max(ns - 3, 0);
-  LI_UNIT_TRACE(0, ns);
 
   const float sc = a.scale * kLog2eMfma;
   int pos[2];
@@ -725,31 +683,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // LDS latency at every fragment).
   constexpr int kVFrags = 2 * kBlk;    // V^T fragments of a stage (two reads each)
   constexpr int kKFrags = 4 * kSteps;  // K fragments of a stage (one read each)
-#ifndef LI_PP_AHEAD
-#define LI_PP_AHEAD 4
-#endif
-  constexpr int kAhead = LI_PP_AHEAD;  // fragments read ahead of the MFMAs that use them
-#ifndef LI_DIAG_NOLDS
-#define LI_DIAG_NOLDS 0
-#endif
+  constexpr int kAhead = 4;  // fragments read ahead of the MFMAs that use them
   auto read_v = [&](uint32_t vb, Frag (&vf)[2][kBlk]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int blk = 0; blk < kBlk; ++blk) {
         const uint32_t tb = vb + t * kHalf;
-        if (LI_DIAG_NOLDS == 1 || LI_DIAG_NOLDS == 2) vf[t][blk] = qf[t][blk % kSteps];
-        else vf[t][blk] = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + L::kRow16);
+        vf[t][blk] = lds_read_vt<Frag>(voff[blk] + tb, voff[blk] + tb + L::kRow16);
       }
   };
   auto read_k = [&](uint32_t kb, Frag (&kf)[4][kSteps]) __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int j = 0; j < kSteps; ++j) {
-        if (LI_DIAG_NOLDS == 1 || LI_DIAG_NOLDS == 3) kf[b][j] = qf[b & 1][(j + b) % kSteps];
-        else kf[b][j] = lds_read_frag<Frag>(koff[j] + kb + (b >> 1) * kHalf + (b & 1) * L::kRow16);
-      }
+      for (int j = 0; j < kSteps; ++j) kf[b][j] = lds_read_frag<Frag>(koff[j] + kb + (b >> 1) * kHalf + (b & 1) * L::kRow16);
   };
   auto pv_mfma = [&](const Frag (&vf)[2][kBlk]) __attribute__((always_inline)) {
 #pragma unroll
@@ -877,7 +825,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int J = decltype(j_tag)::value;
     using Cur = std::integral_constant<int, J>;
     using Prev = std::integral_constant<int, (J + kPpRing - 1) % kPpRing>;
-    LI_TRACE(0);
     // Only stages that exist are loaded, so near the end fewer loads are
     // newer than the one waited for.
     if (!late) {
@@ -885,7 +832,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       else li_wait_vm<0>();
     }
     lds_barrier();
-    LI_TRACE(1);
     // The old value is first read after the unit's last wait for every
     // load, where the compiler places its wait for the atomic (this file is
     // built with the wave-level atomic optimizer off, which would otherwise
@@ -894,28 +840,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!idle) {
       // The matrix phase issues ahead of the other wave's vector work on
       // its SIMD: an MFMA that waits for issue leaves the matrix core idle.
-      LI_SETPRIO_HI();
+      __builtin_amdgcn_s_setprio(kPpMatrixPriority);
       mphase(Prev{}, Cur{});
-      LI_SETPRIO_LO();
+      __builtin_amdgcn_s_setprio(0);
     }
-    LI_TRACE(2);
     if (late) {
       if (j + 2 < ns) li_wait_vm<kWaveDma>();
       else li_wait_vm<0>();
     }
     lds_barrier();
-    LI_TRACE(3);
     if (j < ns) {
       const int st = j + (late ? 3 : 2);
       if (!late && st % kSlotHalfStages == 0 && st + kSlotHalfStages < ns)
         stage_slots_loaders((st + kSlotHalfStages) * kStageKeys, kSlotRing / 2);
       if (st < ns) issue((J + (late ? 3 : 2)) % kPpRing, st);
-      LI_TRACE(4);
       if (!idle) vphase(j * kStageKeys, Cur{});
     }
   };
 
-  LI_TRACE(6);
   // Prologue: slots; the V rows of the last buffer zeroed (the first M
   // phase's P V reads them, with zero weights); stages 0 and 1 in flight,
   // and waves 4-7's share of stage 2.
@@ -961,9 +903,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   lds_barrier();
   if (!late) lds_barrier();  // the barrier waves 4-7 took first
   if (tid == 0) s_unit = next_unit;
-  LI_TRACE(8);
-  LI_UNIT_TRACE(1, ns);
-  LI_TRACE(7);
 
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
@@ -979,7 +918,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       *reinterpret_cast<uint2*>(orow + 16 * blk) = wv;
     }
   }
-  LI_TRACE(9);
   }  // units
 }
 
@@ -1105,37 +1043,17 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
   if (a.kv_fp8) {
     if (dtype == LI_BF16) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true>), g, block, 0, s, a);
     else hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true>), g, block, 0, s, a);
-  } else if (LI_PREFILL_PIPE) {
-    if (dtype == LI_BF16) {
-      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_bf16, 128>), g, block, 0, s, a);
-      else hipLaunchKernelGGL((prefill_pp<li_bf16, 64>), g, block, 0, s, a);
-    } else {
-      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_f16, 128>), g, block, 0, s, a);
-      else hipLaunchKernelGGL((prefill_pp<li_f16, 64>), g, block, 0, s, a);
-    }
   } else if (dtype == LI_BF16) {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, false>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_bf16, 64, W, false>), g, block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_bf16, 128>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_pp<li_bf16, 64>), g, block, 0, s, a);
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, false>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_f16, 64, W, false>), g, block, 0, s, a);
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_f16, 128>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_pp<li_f16, 64>), g, block, 0, s, a);
   }
   return check_launch("prefill_mfma");
 }
 
 int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) { return launch_prefill_waves<kWaves>(in, dtype, s); }
 
-#ifdef LI_PREFILL_TRACE
-extern "C" int li_prefill_trace(long long* host) {
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pp_trace), sizeof(g_pp_trace));
-}
-extern "C" int li_prefill_unit_trace(long long* host) {
-  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pp_units), sizeof(g_pp_units));
-}
-extern "C" int li_prefill_unit_trace_clear() {
-  static long long zero[256][64];
-  return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_pp_units), zero, sizeof(zero));
-}
-#endif
 
 }  // namespace li
