@@ -97,6 +97,41 @@ struct DecodeState {
   floatx4_t acc[8];
 };
 
+// The query operand of one KV head's group, as the score MFMAs take it
+// (B = Q^T; lane (n, g) holds head n, zeros past the group's heads).
+//
+// 16-bit pools: D / 32 fragments of the query (v_mfma_f32_16x16x32_*),
+// lane (n, g) holding dims 32 j + 8 g .. + 8 of fragment j.
+//
+// fp8 pools: the scores run on v_mfma_scale_f32_16x16x128_f8f6f4 with K
+// straight from the pool bytes (no conversion of K), so the query is given
+// in e4m3 as well: head n's row is scaled by an exact power of two 2^e that
+// puts its largest |value| in [128, 256), then split into kTerms e4m3 terms,
+// each the rounding of what the terms before it left. A bf16 value has 8
+// significant bits and an fp16 value 11; two (three) 4-bit terms hold them
+// exactly, except for values below the e4m3 normal range (2^-6, i.e. under
+// 2^-13 of the row's largest), whose last term keeps them to within 2^-10
+// -- 2^-17 of the largest. The terms' MFMAs chain into one accumulator and
+// `scale` (2^-e) returns the scores to the query's units. Lane (n, g) holds
+// dims 32 g .. 32 g + 31 of head n, byte i of each term being dim 32 g + i,
+// the same order in which it reads the K bytes of its key, so the two
+// operands meet dim for dim.
+typedef int v8i_t __attribute__((ext_vector_type(8)));
+
+template <typename T, int D, bool F8>
+struct DecodeQuery {
+  typename Mfma<T>::Frag f[D / 32];
+  float scale;  // 1
+};
+
+template <typename T, int D>
+struct DecodeQuery<T, D, true> {
+  static_assert(D == 128, "fp8 pools: head_dim 128");
+  static constexpr int kTerms = std::is_same<T, li_f16>::value ? 3 : 2;
+  v8i_t t[kTerms];
+  float scale;  // 2^-e
+};
+
 // Per-lane LDS byte offsets within a tile: the K operand of key n, step j
 // (key 16 + n sits L::kRow16 bytes below), and the V^T reads' addresses
 // (li_read_vt's two for 16-bit rows, the one 8-bit transposing read for
@@ -104,13 +139,14 @@ struct DecodeState {
 template <int D, bool F8>
 struct TileOffsets {
   uint32_t koff[D / 32], voff[D / 16];
+  uint32_t kq[2];  // fp8: the two 16-byte chunks (dims 32 g ..) of key n's K row
   __device__ __forceinline__ TileOffsets() {
     using L = KvTile<D, F8>;
     const int lane = threadIdx.x;
     const int n = lane & 15, g = lane >> 4;
     if constexpr (F8) {
-#pragma unroll
-      for (int j = 0; j < D / 32; ++j) koff[j] = L::offset(n, 2 * j + (g >> 1)) + 8 * (g & 1);
+      kq[0] = L::offset(n, 2 * g);
+      kq[1] = L::offset(n, 2 * g + 1);
       const int s16 = lane & 15;
 #pragma unroll
       for (int blk = 0; blk < D / 16; ++blk) voff[blk] = L::voffset(kappa(g, s16 >> 1), blk) + 8 * (s16 & 1);
@@ -125,11 +161,11 @@ struct TileOffsets {
 };
 
 // Folds the 32-key tile in `stage` (LDS byte address) whose first key is t0
-// into `st`; keys at or past `te` are masked. qf holds this lane's head's
-// query (zeros for heads past the group), sc the softmax scale times log2(e)
-// (and an fp8 pool's k_scale).
+// into `st`; keys at or past `te` are masked. q holds the group's query, sc
+// the softmax scale times log2(e) (and an fp8 pool's k_scale, and the
+// query's scale q.scale).
 template <typename T, int D, bool F8>
-__device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const typename Mfma<T>::Frag* qf, float sc,
+__device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const DecodeQuery<T, D, F8>& q, float sc,
                                           const TileOffsets<D, F8>& o, DecodeState& st) {
   using M = Mfma<T>;
   using Frag = typename M::Frag;
@@ -138,14 +174,25 @@ __device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const 
   const int lane = threadIdx.x;
   const int g = lane >> 4;
   floatx4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (F8) {
+    // Keys n and 16 + n, dims 32 g .. 32 g + 31, as stored (e4m3).
+    auto krow = [&](uint32_t at) {
+      const u32x4_t lo = *(const __attribute__((address_space(3))) u32x4_t*)(uintptr_t)(at + o.kq[0]);
+      const u32x4_t hi = *(const __attribute__((address_space(3))) u32x4_t*)(uintptr_t)(at + o.kq[1]);
+      return v8i_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    };
+    const v8i_t k0 = krow(stage), k1 = krow(stage + L::kRow16);
 #pragma unroll
-  for (int j = 0; j < kSteps; ++j) {
-    if constexpr (F8) {
-      s0 = M::mma(lds_read_f8_frag<Frag>(stage + o.koff[j]), qf[j], s0);
-      s1 = M::mma(lds_read_f8_frag<Frag>(stage + o.koff[j] + L::kRow16), qf[j], s1);
-    } else {
-      s0 = M::mma(lds_read_frag<Frag>(stage + o.koff[j]), qf[j], s0);
-      s1 = M::mma(lds_read_frag<Frag>(stage + o.koff[j] + L::kRow16), qf[j], s1);
+    for (int t = 0; t < DecodeQuery<T, D, F8>::kTerms; ++t) {
+      // Formats e4m3 (0) for both operands, block scales 2^0 (e8m0 127).
+      s0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k0, q.t[t], s0, 0, 0, 0, 127, 0, 127);
+      s1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k1, q.t[t], s1, 0, 0, 0, 127, 0, 127);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSteps; ++j) {
+      s0 = M::mma(lds_read_frag<Frag>(stage + o.koff[j]), q.f[j], s0);
+      s1 = M::mma(lds_read_frag<Frag>(stage + o.koff[j] + L::kRow16), q.f[j], s1);
     }
   }
   float x[8];
@@ -191,9 +238,8 @@ __device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const 
 }
 
 // Folds keys [kb, ke) of sequence `seq`'s context for KV head `kvh` into `st`.
-// qf holds this lane's head's query (zeros for heads past the group).
 template <typename T, int D, bool F8>
-__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& lds, const typename Mfma<T>::Frag* qf,
+__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& lds, const DecodeQuery<T, D, F8>& q,
                                           int seq, int kvh, int kb, int ke, DecodeState& st) {
   using L = KvTile<D, F8>;
   const int lane = threadIdx.x;
@@ -204,7 +250,7 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& l
   const uint32_t row_bytes = (uint32_t)(a.p_s0 * esize);
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
   // An fp8 pool stores K / k_scale: its scale multiplies the scores.
-  const float sc = a.scale * (F8 ? a.k_scale : 1.f) * kLog2eMfma;
+  const float sc = a.scale * (F8 ? a.k_scale * q.scale : 1.f) * kLog2eMfma;
 
   for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
     const int c1 = min(c0 + kSlotChunk, ke);
@@ -222,7 +268,7 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& l
     }
 
     auto fold = [&](uint32_t stage, int t0) __attribute__((always_inline)) {
-      fold_tile<T, D, F8>(stage, t0, c1, qf, sc, off, st);
+      fold_tile<T, D, F8>(stage, t0, c1, q, sc, off, st);
     };
 
     // Two stages: while one tile is folded the next tile's loads land in the
@@ -246,15 +292,57 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& l
   }
 }
 
-// Loads the query fragments of KV head `kvh`'s group for the query at `row`.
-template <typename T, int D>
-__device__ __forceinline__ void load_query(const AttnArgs& a, int row, int kvh, typename Mfma<T>::Frag* qf) {
+// Loads the query operand of KV head `kvh`'s group for the query at `row`.
+template <typename T, int D, bool F8>
+__device__ __forceinline__ void load_query(const AttnArgs& a, int row, int kvh, DecodeQuery<T, D, F8>& q) {
   using Frag = typename Mfma<T>::Frag;
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
-  const T* qrow = static_cast<const T*>(a.q) + (int64_t)row * a.q_s0 + (int64_t)(kvh * a.groups + n) * a.q_s1 + 8 * g;
+  const T* qrow = static_cast<const T*>(a.q) + (int64_t)row * a.q_s0 + (int64_t)(kvh * a.groups + n) * a.q_s1;
+  if constexpr (!F8) {
 #pragma unroll
-  for (int j = 0; j < D / 32; ++j) qf[j] = (n < a.groups) ? *reinterpret_cast<const Frag*>(qrow + 32 * j) : Frag{};
+    for (int j = 0; j < D / 32; ++j) q.f[j] = (n < a.groups) ? *reinterpret_cast<const Frag*>(qrow + 32 * j + 8 * g) : Frag{};
+    q.scale = 1.f;
+  } else {
+    float x[32];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const Frag f = (n < a.groups) ? *reinterpret_cast<const Frag*>(qrow + 32 * g + 8 * i) : Frag{};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)f[e];
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    amax = li_group_max(amax);  // the head's four lanes
+    // amax in [2^(E-127), 2^(E-126)): 2^(134-E) puts it in [2^7, 2^8).
+    const int ex = min(max(134 - (int)((__float_as_uint(amax) >> 23) & 0xff), -126), 126);
+    const float mult = __uint_as_float((uint32_t)(127 + ex) << 23);
+    q.scale = __uint_as_float((uint32_t)(127 - ex) << 23);
+#pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] *= mult;
+    typedef short s2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int t = 0; t < DecodeQuery<T, D, F8>::kTerms; ++t) {
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        s2_t b = {0, 0};
+        b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(b, x[4 * w], x[4 * w + 1], 1.f, false);
+        b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(b, x[4 * w + 2], x[4 * w + 3], 1.f, true);
+        const uint32_t bits = __builtin_bit_cast(uint32_t, b);
+        q.t[t][w] = (int)bits;
+        if (t + 1 < DecodeQuery<T, D, F8>::kTerms) {
+          // What this term left: exact in fp32.
+          const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, false);
+          const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, true);
+          x[4 * w] -= lo[0];
+          x[4 * w + 1] -= lo[1];
+          x[4 * w + 2] -= hi[0];
+          x[4 * w + 3] -= hi[1];
+        }
+      }
+    }
+  }
 }
 
 // Writes a finished softmax: the normalised output row of each head of the
@@ -319,7 +407,6 @@ __device__ __forceinline__ int decode_keys(const AttnArgs& a, int seq) {
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool F8>
 __global__ __launch_bounds__(64) void decode_partitioned(AttnArgs a) {
-  using Frag = typename Mfma<T>::Frag;
   __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds;
   const float vscale = F8 ? a.v_scale : 1.f;
   // Partition-major order: every sequence's first partition is dispatched
@@ -347,11 +434,11 @@ __global__ __launch_bounds__(64) void decode_partitioned(AttnArgs a) {
   const int ke = min(kb + plen, ctx);
   const int nparts = (ctx + plen - 1) / plen;
 
-  Frag qf[D / 32];
-  load_query<T, D>(a, row, kvh, qf);
+  DecodeQuery<T, D, F8> q;
+  load_query(a, row, kvh, q);
   DecodeState st;
   reset_state(st);
-  fold_keys<T, D, F8>(a, lds, qf, seq, kvh, kb, ke, st);
+  fold_keys<T, D, F8>(a, lds, q, seq, kvh, kb, ke, st);
   const int head0 = kvh * a.groups;
   if (nparts == 1) {
     store_state<T, D>(st, static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head0 * a.o_s1, a.o_s1,
@@ -402,7 +489,6 @@ __device__ __forceinline__ void balanced_share(const AttnArgs& a, int64_t& total
 
 template <typename T, int D, bool F8>
 __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
-  using Frag = typename Mfma<T>::Frag;
   __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds;
   const float vscale = F8 ? a.v_scale : 1.f;
   const int lane = threadIdx.x;
@@ -462,11 +548,11 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
           int4{w, (int)((off + ctx - 1) / share), first_segment ? 0 : 1, 0};
     }
     const int row = decode_row(a, seq);
-    Frag qf[D / 32];
-    load_query<T, D>(a, row, kvh, qf);
+    DecodeQuery<T, D, F8> q;
+    load_query(a, row, kvh, q);
     DecodeState st;
     reset_state(st);
-    fold_keys<T, D, F8>(a, lds, qf, seq, kvh, key0, key0 + take, st);
+    fold_keys<T, D, F8>(a, lds, q, seq, kvh, key0, key0 + take, st);
     if (key0 == 0 && take == ctx) {
       store_state<T, D>(st, static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)kvh * G * a.o_s1, a.o_s1,
                         nullptr, nullptr, 0, G, vscale);
@@ -507,7 +593,6 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
 // ---------------------------------------------------------------------------
 template <typename T, int D, bool F8, int HG>
 __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
-  using Frag = typename Mfma<T>::Frag;
   using L = KvTile<D, F8>;
   static_assert(HG % 2 == 0, "an even head count keeps every ring stage index a constant");
   __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds;
@@ -597,11 +682,11 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
             int4{w, (int)((seg + nu - 1) / share), first_segment ? 0 : 1, 0};
       }
       const int row = decode_row(a, seq);
-      Frag qf[HG][D / 32];
+      DecodeQuery<T, D, F8> q[HG];
       DecodeState st[HG];
 #pragma unroll
       for (int h = 0; h < HG; ++h) {
-        load_query<T, D>(a, row, h0 + h, qf[h]);
+        load_query(a, row, h0 + h, q[h]);
         reset_state(st[h]);
       }
       const char* kbase = static_cast<const char*>(a.kp) + h0 * head_bytes;
@@ -631,7 +716,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
             issue_tile<D, F8>(lds.stage[(h + 1) & 1], kbase + nh * head_bytes, vbase + nh * head_bytes, lds.sl,
                               row_bytes, min(32 * nt, kSlotChunk), lane);
             li_wait_vm<kInFlight>();
-            fold_tile<T, D, F8>(lds_addr(lds.stage[h & 1]), c0 + 32 * ti, c1, qf[h], sc, off, st[h]);
+            fold_tile<T, D, F8>(lds_addr(lds.stage[h & 1]), c0 + 32 * ti, c1, q[h], sc * q[h].scale, off, st[h]);
           }
         }
         li_wait_vm<0>();

@@ -100,6 +100,31 @@ def test_fp8_decode_groupings(num_heads, num_kv_heads):
     assert_within(out, want, 2e-2, 2e-3)
 
 
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
+def test_fp8_decode_queries_of_any_scale(q_dtype):
+    """The fp8 scores take the query as e4m3 terms after a power-of-two scale per head: heads
+    at 2^-20 .. 2^12 of the usual size, an all-zero head, and rows whose elements spread over
+    16 binades all meet the bar."""
+    b, kp, vp, _ = _fp8_batch([5, 64, 700, 2049], 0.5, 0.25, q_dtype=q_dtype, seed=9, num_slots=8192)
+    g = torch.Generator(device="cpu").manual_seed(3)
+    q = b.query.float().cpu()
+    spread = torch.pow(2.0, -torch.randint(0, 17, q.shape, generator=g).float())
+    q[:, 1::4] *= spread[:, 1::4]
+    head_scale = torch.tensor([2.0 ** -20, 1.0, 2.0 ** -6, 2.0 ** 5] * (q.shape[1] // 4))
+    if q_dtype == torch.bfloat16:
+        head_scale[3::8] = 2.0 ** 12
+    q *= head_scale.view(1, -1, 1)
+    q[:, 2] = 0.0
+    b.query = q.to(q_dtype).to(DEV)
+    kd = fp8.dequantize(_codes(kp), 0.5)
+    vd = fp8.dequantize(_codes(vp), 0.25)
+    want = attend(to_numpy(b.query), kd, vd, b.slot_table.cpu().numpy(), np.asarray(b.context_lens), b.scaling,
+                  b.groups, dtype=np.float64)
+    out = paged_decode(b.query, kp, vp, b.slot_table, b.context_lens_t, b.scaling, b.groups, k_scale=0.5,
+                       v_scale=0.25)
+    assert_within(out, want, 2e-2, 2e-3)
+
+
 def test_c2_fp8_pool_full_size_and_against_the_bf16_cache():
     """Config 2's decode step on an fp8 pool: at the bf16 bar against the oracle over the
     dequantised rows, and within a bounded distance of the same step on the bf16 pool."""
