@@ -560,6 +560,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Work-group barriers here order LDS only (lds_barrier): a unit's output
   // stores and the loads in flight never hold a barrier up.
   __shared__ int s_unit;
+  __shared__ int s_rows[3];  // the unit's first token + q0, its query count, first head
   if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
   int next_unit = 0;  // tid 0: the unit claimed for after this one
   for (;;) {
@@ -592,6 +593,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // atomic's round trip is hidden, yet late enough that a work-group that
   // finishes early still takes the heaviest unit left.
   const int claim_at = max(ns - 3, 0);
+  // Read by the epilogue, after the key loop (the barriers between order it).
+  if (tid == 0) {
+    s_rows[0] = first_tok + q0;
+    s_rows[1] = q1 - q0;
+    s_rows[2] = kvh * G;
+  }
+
+  // The unit's first slots (the whole ring, or the unit's keys if fewer)
+  // are read here, before the queries, and written to the ring in the
+  // prologue: both reads share one round trip.
+  const int64_t* srow = a.st + (int64_t)seq * a.st_s;
+  constexpr int kSlotsPer = kSlotRing / (64 * W);
+  int first_slots[kSlotsPer];
+#pragma unroll
+  for (int r = 0; r < kSlotsPer; ++r) first_slots[r] = (int)srow[min(tid + r * 64 * W, kend - 1)];
 
   const float sc = a.scale * kLog2eMfma;
   int pos[2];
@@ -626,7 +642,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   const char* kpool = static_cast<const char*>(a.kp) + (int64_t)kvh * a.p_s1 * (int)sizeof(T);
   const char* vpool = static_cast<const char*>(a.vp) + (int64_t)kvh * a.p_s1 * (int)sizeof(T);
-  const int64_t* srow = a.st + (int64_t)seq * a.st_s;
   const uint32_t row_bytes = (uint32_t)(a.p_s0 * (int)sizeof(T));
 
   // Running row maxima m (log2 units; -inf before the first stage) and
@@ -654,9 +669,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Slot ring: entry k % kSlotRing holds key k's slot (keys past the block's
   // last one repeat it, so every load reads a real row).
-  auto stage_slots = [&](int k0, int count) {
-    for (int i = tid; i < count; i += 64 * W) sl[(k0 + i) % kSlotRing] = (int)srow[min(k0 + i, kend - 1)];
-  };
   auto stage_slots_loaders = [&](int k0, int count) {  // waves 0-3
     for (int i = tid; i < count; i += 256) sl[(k0 + i) % kSlotRing] = (int)srow[min(k0 + i, kend - 1)];
   };
@@ -865,7 +877,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
     for (int t = 0; t < 2; ++t) pf[nb][t] = Frag{};
-  stage_slots(0, min(kSlotRing, ns * kStageKeys));
+#pragma unroll
+  for (int r = 0; r < kSlotsPer; ++r) sl[tid + r * 64 * W] = first_slots[r];
   for (int i = tid; i < kRegion / 16; i += 64 * W)
     *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(
         (uintptr_t)(lds_addr(vst[kPpRing - 1]) + 16 * i)) = u32x4_t{0u, 0u, 0u, 0u};
@@ -904,18 +917,56 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (!late) lds_barrier();  // the barrier waves 4-7 took first
   if (tid == 0) s_unit = next_unit;
 
+  // The output rows, normalised. A lane holds 8-byte pieces of its row 32
+  // bytes apart, so stored as they are every store instruction would write
+  // 16 rows' 32-byte pieces; instead each wave stages its 32 rows in its own
+  // slice of the (now unused) K region -- rows of kRowBytes, 16-byte chunk
+  // c of row r at slot c ^ (r mod kCh), so the 16 rows a write spans hit
+  // different banks -- and stores whole chunks, kCh lanes per row: each
+  // instruction writes 64 / kCh whole rows (the G heads of a query are
+  // adjacent rows of the output, so mostly one contiguous span).
+  if (!idle) {
+    constexpr int kCh = L::kRowBytes / 16;
+    // The lane index through an empty asm: the addresses below are then
+    // computed here, not hoisted out of the unit loop into registers that
+    // the key loop cannot spare.
+    int el = lane;
+    asm volatile("" : "+v"(el));
+    const int en = el & 15, eg = el >> 4;
+    const uint32_t ebase = lds_addr(&kst[0][0]) + (uint32_t)w * (32 * L::kRowBytes);
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const float lt = acc[nb][kBlk][0];
-    if (!real[nb]) continue;
-    const float inv = 1.f / lt;
-    T* orow = static_cast<T*>(a.out) + (int64_t)tok[nb] * a.o_s0 + (int64_t)head[nb] * a.o_s1 + 4 * g;
+    for (int nb = 0; nb < 2; ++nb) {
+      const float inv = 1.f / acc[nb][kBlk][0];
+      const int r = 16 * nb + en;
 #pragma unroll
-    for (int blk = 0; blk < kBlk; ++blk) {
-      uint2 wv;
-      wv.x = li_pack2<T>(acc[nb][blk][0] * inv, acc[nb][blk][1] * inv);
-      wv.y = li_pack2<T>(acc[nb][blk][2] * inv, acc[nb][blk][3] * inv);
-      *reinterpret_cast<uint2*>(orow + 16 * blk) = wv;
+      for (int blk = 0; blk < kBlk; ++blk) {
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t wv = {li_pack2<T>(acc[nb][blk][0] * inv, acc[nb][blk][1] * inv),
+                            li_pack2<T>(acc[nb][blk][2] * inv, acc[nb][blk][3] * inv)};
+        const int c = 2 * blk + (eg >> 1);  // the piece: bytes 32 blk + 8 g of the row
+        *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(
+            (uintptr_t)(ebase + r * L::kRowBytes + 16 * (c ^ (r % kCh)) + 8 * (eg & 1))) = wv;
+      }
+    }
+    constexpr int kRowsPer = 64 / kCh;  // rows one store instruction covers
+    const int c = el % kCh;
+    // The unit's rows, as recorded at its start (kept in LDS rather than
+    // registers through the key loop).
+    const int tok0 = __builtin_amdgcn_readfirstlane(s_rows[0]);
+    const int nvalid = __builtin_amdgcn_readfirstlane(s_rows[1]);
+    const int head0 = __builtin_amdgcn_readfirstlane(s_rows[2]);
+#pragma unroll
+    for (int i = 0; i < 32 / kRowsPer; ++i) {
+      const int r = el / kCh + kRowsPer * i;
+      const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+          (uintptr_t)(ebase + r * L::kRowBytes + 16 * (c ^ (r % kCh))));
+      const int row = 32 * w + r;
+      const int ql = row / a.groups;
+      if (ql < nvalid) {  // (so row < block_q * G too)
+        T* orow = static_cast<T*>(a.out) + (int64_t)(tok0 + ql) * a.o_s0 +
+                  (int64_t)(head0 + row % a.groups) * a.o_s1 + 8 * c;
+        *reinterpret_cast<u32x4_t*>(orow) = v;
+      }
     }
   }
   }  // units
