@@ -893,8 +893,8 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
   const dim3 grid((unsigned)blocks), block(64);
 #define LI_DECODE_LAUNCH(T, D, F8)                                                                   \
   do {                                                                                               \
-    if (!F8 && balanced && a.part_heads == kDecodeHeadGroup)                                         \
-      hipLaunchKernelGGL((decode_grouped<T, D, false, kDecodeHeadGroup>), grid, block, 0, s, a);     \
+    if (balanced && a.part_heads == kDecodeHeadGroup)                                                \
+      hipLaunchKernelGGL((decode_grouped<T, D, F8, kDecodeHeadGroup>), grid, block, 0, s, a);        \
     else if (balanced) hipLaunchKernelGGL((decode_balanced<T, D, F8>), grid, block, 0, s, a);        \
     else hipLaunchKernelGGL((decode_partitioned<T, D, F8>), grid, block, 0, s, a);                   \
   } while (0)

@@ -74,12 +74,12 @@ int balanced_waves(int num_cus) {
 }
 
 // KV heads per partial slot of the balanced split: kDecodeHeadGroup when
-// the head-grouped kernel serves the shape (a 16-bit pool, num_kv_heads a
-// multiple of the group), else one. Grouping pays on 16-bit pools (config 2:
-// 204 -> 196 us) and costs on fp8 ones (config 4: 191 -> 200 us), whose
-// per-head rows are already half as long.
-int balanced_part_heads(int num_kv_heads, bool kv_fp8) {
-  return !kv_fp8 && num_kv_heads % kDecodeHeadGroup == 0 ? kDecodeHeadGroup : 1;
+// the head-grouped kernel serves the shape (num_kv_heads a multiple of the
+// group), else one. Grouping pays on 16-bit pools (config 2: 204 -> 196 us)
+// and on fp8 ones, whose scores run on the fp8 matrix cores (config 2:
+// 112.5 -> 108 us; config 4 unchanged; four heads per wave: 116 / 208 us).
+int balanced_part_heads(int num_kv_heads) {
+  return num_kv_heads % kDecodeHeadGroup == 0 ? kDecodeHeadGroup : 1;
 }
 
 // What starting a segment (its query, its slots, the ring's first tile)
@@ -89,7 +89,7 @@ int segment_cost() { return kSegmentCost; }
 
 size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads) {
   // Sized for either pool type (the plan calls do not know it).
-  const size_t rows = (size_t)waves * 2 * groups * balanced_part_heads(num_kv_heads, false);
+  const size_t rows = (size_t)waves * 2 * groups * balanced_part_heads(num_kv_heads);
   return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) +
          align256((size_t)batch * num_kv_heads * 16);
 }
@@ -98,7 +98,7 @@ size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int nu
 void set_balanced(AttnArgs& d, int waves, void* workspace) {
   d.num_parts = waves;
   d.part_len = -1;
-  d.part_heads = balanced_part_heads(d.num_kv_heads, d.kv_fp8 != 0);
+  d.part_heads = balanced_part_heads(d.num_kv_heads);
   d.seg_cost = segment_cost();
   const size_t rows = (size_t)waves * 2 * d.groups * d.part_heads;
   char* p = static_cast<char*>(workspace);
