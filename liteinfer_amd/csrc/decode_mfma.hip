@@ -758,12 +758,13 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
 // head), reading the piece range the wave holding the context's first key
 // recorded; a context no wave boundary cut was written directly. Up to
 // eight pieces (the usual case), every piece's LSE and partial row load at
-// once; beyond that, lane k holds piece k's weight (64 pieces at a time) and
-// the partial rows are read eight pieces at a time so their loads overlap.
+// once; beyond that, in rounds of 32 pieces whose LSEs and partial rows load
+// together.
 template <typename T>
 __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
-  constexpr int kMaxC = kGenericMaxHeadDim / 64;
+  constexpr int kMaxC = kMfmaMaxHeadDim / 64;  // dims per lane
   constexpr int kBatch = 8;
+  constexpr int kWide = 32;
   const int lane = threadIdx.x;
   const int head = blockIdx.x % a.num_heads;
   const int seq = blockIdx.x / a.num_heads;
@@ -831,35 +832,40 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
     return;
   }
 
-  float mx = -INFINITY;
-  for (int j = lane; j < n; j += 64) mx = fmaxf(mx, a.part_lse[row_of(j)]);
-  mx = li_wave_max(mx);
+  // More pieces (long contexts over few sequences): rounds of kWide
+  // pieces, each round's LSEs and partial rows loaded together (one round
+  // trip per round) and folded into a running maximum, sum and row,
+  // rescaled when the maximum grows.
+  float m = -INFINITY, wsum = 0.f;
   float acc[kMaxC];
 #pragma unroll
   for (int c = 0; c < kMaxC; ++c) acc[c] = 0.f;
-  float wsum = 0.f;
-  for (int j0 = 0; j0 < n; j0 += 64) {
-    const int jn = min(64, n - j0);
-    const float wl = lane < jn ? exp2f(a.part_lse[row_of(j0 + lane)] - mx) : 0.f;
-    wsum += li_wave_sum(wl);
-    for (int kb = 0; kb < jn; kb += kBatch) {
-      float v[kBatch][kMaxC];
+  for (int j0 = 0; j0 < n; j0 += kWide) {
+    const int jn = min(kWide, n - j0);
+    const float lse = lane < jn ? a.part_lse[row_of(j0 + lane)] : -INFINITY;
+    float v[kWide][kMaxC];
 #pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        const float* po = a.part_o + row_of(min(j0 + kb + k, n - 1)) * D;
+    for (int k = 0; k < kWide; ++k) {
+      const float* po = a.part_o + row_of(j0 + min(k, jn - 1)) * D;
 #pragma unroll
-        for (int c = 0; c < kMaxC; ++c) {
-          const int d = lane + 64 * c;
-          v[k][c] = (kb + k < jn && d < D) ? po[d] : 0.f;
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < kBatch; ++k) {
-        const float wt = __shfl(wl, (kb + k) & 63, 64);
-#pragma unroll
-        for (int c = 0; c < kMaxC; ++c) acc[c] = fmaf(wt, v[k][c], acc[c]);
+      for (int c = 0; c < kMaxC; ++c) {
+        const int d = lane + 64 * c;
+        v[k][c] = (k < jn && d < D) ? po[d] : 0.f;
       }
     }
+    const float nm = fmaxf(m, li_wave_max(lse));
+    const float keep = m == -INFINITY ? 0.f : exp2f(m - nm);
+    const float wl = lane < jn ? exp2f(lse - nm) : 0.f;
+    wsum = wsum * keep + li_wave_sum(wl);
+#pragma unroll
+    for (int c = 0; c < kMaxC; ++c) acc[c] *= keep;
+#pragma unroll
+    for (int k = 0; k < kWide; ++k) {
+      const float wt = __shfl(wl, k, 64);
+#pragma unroll
+      for (int c = 0; c < kMaxC; ++c) acc[c] = fmaf(wt, v[k][c], acc[c]);
+    }
+    m = nm;
   }
   const float inv = 1.f / wsum;
 #pragma unroll

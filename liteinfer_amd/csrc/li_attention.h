@@ -64,6 +64,8 @@ constexpr int kDecodeHeadGroup = LI_DECODE_HEAD_GROUP;
 
 // Largest head_dim the general-shape kernel serves.
 constexpr int kGenericMaxHeadDim = 512;
+// Largest head_dim the MFMA decode and prefill kernels serve (64 or 128).
+constexpr int kMfmaMaxHeadDim = 128;
 
 int launch_attend_generic(const AttnArgs& a, int dtype, hipStream_t s);
 int launch_combine(const AttnArgs& a, int dtype, hipStream_t s);
