@@ -158,6 +158,17 @@ def test_long_context_is_partitioned_and_combined():
     assert_within(_run(b), b.oracle(), 2e-2, 2e-3)
 
 
+@pytest.mark.parametrize(("context_lens", "num_kv_heads"), [([60000], 1), ([40000, 9], 2), ([120000], 2)])
+def test_a_context_cut_into_hundreds_of_pieces(context_lens, num_kv_heads):
+    """One long sequence over one or two KV heads: the balanced grid cuts each
+    (sequence, KV head) into hundreds of pieces, which the combine folds in
+    rounds of 32 with a running maximum (dozens of rounds here); a 9-key
+    sequence beside it stays whole in one wave."""
+    b = PagedBatch(context_lens, dtype=torch.bfloat16, num_heads=4 * num_kv_heads, num_kv_heads=num_kv_heads,
+                   head_dim=128, num_slots=131072, seed=23)
+    assert_within(_run(b), b.oracle(), 2e-2, 2e-3)
+
+
 @pytest.mark.parametrize(("num_heads", "num_kv_heads", "head_dim"), [(32, 8, 128), (16, 1, 64), (12, 6, 128)])
 def test_more_sequences_than_a_wave_has_lanes(num_heads, num_kv_heads, head_dim):
     """150 sequences: the balanced kernels find a wave's first sequence and
