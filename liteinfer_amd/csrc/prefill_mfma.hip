@@ -1000,11 +1000,15 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
     *tiles = (a.ctx[seq] + 31) / 32;
     return min((nq + a.block_q - 1) / a.block_q, a.num_qblocks);
   };
+  // A thread's first sequence (the only one while batch <= 1024) is read
+  // once and kept for all three passes; further ones are read again.
+  int c_t = 0;
+  const int c_nb = tid < a.batch ? blocks_of(tid, &c_t) : 0;
   if (tid < kOrderBins) hist[tid] = 0;
   if (tid == 0) max_tiles = 0;
   __syncthreads();
-  int local = 0;
-  for (int sq = tid; sq < a.batch; sq += 1024) {
+  int local = c_t;
+  for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
     int t;
     blocks_of(sq, &t);
     local = max(local, t);
@@ -1017,33 +1021,47 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   while ((max_tiles >> shift) >= kOrderBins) ++shift;
   // Bin b holds the blocks of sequences with (tiles >> shift) ==
   // kOrderBins - 1 - b, so bins run from the heaviest down.
-  for (int sq = tid; sq < a.batch; sq += 1024) {
+  if (c_nb > 0) atomicAdd(&hist[kOrderBins - 1 - (c_t >> shift)], c_nb);
+  for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
     int t;
     const int nb = blocks_of(sq, &t);
     if (nb > 0) atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
   }
   __syncthreads();
-  // Exclusive prefix sum over the bins: Hillis-Steele in LDS.
-  int v = tid < kOrderBins ? hist[tid] : 0;
-  const int own = v;
+  // Exclusive prefix sum over the bins: a scan within each of the first
+  // kOrderBins / 64 waves, then the totals of the waves before.
+  {
+    __shared__ int wave_total[kOrderBins / 64];
+    const int lane = tid & 63;
+    int incl = 0, own = 0;
+    if (tid < kOrderBins) {
+      own = hist[tid];
+      incl = own;
 #pragma unroll
-  for (int d = 1; d < kOrderBins; d *= 2) {
+      for (int off = 1; off < 64; off <<= 1) {
+        const int up = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += up;
+      }
+      if (lane == 63) wave_total[tid >> 6] = incl;
+    }
     __syncthreads();
-    const int add = (tid < kOrderBins && tid >= d) ? hist[tid - d] : 0;
-    __syncthreads();
-    v += add;
-    if (tid < kOrderBins) hist[tid] = v;
+    if (tid < kOrderBins) {
+      int before = 0;
+      for (int v = 0; v < (tid >> 6); ++v) before += wave_total[v];
+      hist[tid] = before + incl - own;
+      if (tid == kOrderBins - 1) max_tiles = before + incl;  // now: the number of blocks listed
+    }
   }
   __syncthreads();
-  if (tid < kOrderBins) hist[tid] = v - own;
-  if (tid == kOrderBins - 1) max_tiles = v;  // now: the number of blocks listed
-  __syncthreads();
-  for (int sq = tid; sq < a.batch; sq += 1024) {
-    int t;
-    const int nb = blocks_of(sq, &t);
-    if (nb == 0) continue;
+  auto place = [&](int sq, int nb, int t) {
     const int at = atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
     for (int i = 0; i < nb; ++i) a.work[at + i] = sq * a.num_qblocks + (nb - 1 - i);
+  };
+  if (c_nb > 0) place(tid, c_nb, c_t);
+  for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
+    int t;
+    const int nb = blocks_of(sq, &t);
+    if (nb > 0) place(sq, nb, t);
   }
   const int items = a.batch * a.num_qblocks;
   for (int i = max_tiles + tid; i < items; i += 1024) a.work[i] = -1;
