@@ -184,56 +184,32 @@ def _paged_decode_step(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_
     return out.unsqueeze(2)
 
 
-# MI355X (gfx950) published peaks. Only their ratio matters to the choice
-# below: it compares the roofline times of two kinds of work on one device.
-_HBM_PEAK_BYTES_PER_S = 8.0e12
-_MFMA_PEAK_FLOPS_PER_S = 2.5e15
-# The prefill kernel folds a one-query sequence's whole context into one
-# work-group, so it takes such rows only while contexts are bounded.
-_LONGEST_ROW_FOR_PREFILL = 8192
+def _one_query_rows_to_decode_kernel(query_lens) -> bool:
+    """Whether a packed pass's one-query sequences should go to the decode split.
 
-
-def _one_query_rows_to_decode_kernel(query_lens, context_lens, num_heads: int, num_kv_heads: int, head_dim: int,
-                                     pool_element_size: int) -> bool:
-    """Whether a packed pass's one-query sequences should go to the decode kernel.
-
-    False (the prefill kernel serves them beside the chunks, in one launch)
-    when there are none, or when streaming their keys has a roofline time
-    (bytes at peak HBM bandwidth) no longer than the chunks' (flops at peak
-    MFMA rate) and no context is longer than ``_LONGEST_ROW_FOR_PREFILL``:
-    the rows' loads then overlap the chunks' matrix work and fill the tail of
-    the persistent queue, where they are queued after the chunk blocks
-    (config 3: rows 0.55x the chunks' roofline time; in-kernel 72 us for rows
-    that take 99 us in their own launch). Once the rows' memory time passes
-    the chunks' matrix time there is nothing left to hide them behind, and
-    the decode kernel's split over the whole grid streams them faster. On fp8
-    pools every prefill stage also converts in LDS, which folded rows would
-    pay too, so they always go to the decode kernel. The answer is the same
-    attention either way; the rule depends on no box-specific rate, only on
-    the ratio of the two peaks.
+    True whenever there are any. Over a 16-bit pool the split runs inside the
+    prefill launch: its first work-groups stream the rows' K/V while the rest
+    fold the chunks on the matrix cores, then join the chunks' queues
+    (``prefill_pp_rows``; config 3: 316-335 us against 341-387 us with the
+    rows folded as prefill units, where each row walks its whole context
+    through a 256-row work-group at matrix-core speed; no case measured
+    slower). Over an fp8 pool the decode kernel runs before the prefill.
+    False (no decode launch, ``LI_FLAG_PREFILL_ONLY``) when there are none;
+    a caller may still ask for the folded form with ``one_query_rows=False``.
+    The answer is the same attention either way.
     """
-    rows = [c for q, c in zip(query_lens, context_lens) if q == 1]
-    if not rows:
-        return False
-    if pool_element_size < 2 or max(rows) > _LONGEST_ROW_FOR_PREFILL:
-        return True
-    row_bytes = sum(rows) * num_kv_heads * head_dim * pool_element_size * 2
-    chunk_flops = sum(4 * num_heads * head_dim * (q * (c - q) + q * (q + 1) / 2)
-                      for q, c in zip(query_lens, context_lens) if q > 1)
-    return row_bytes / _HBM_PEAK_BYTES_PER_S > chunk_flops / _MFMA_PEAK_FLOPS_PER_S
+    return any(q == 1 for q in query_lens)
 
 
 def _paged_packed(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_groups: int) -> torch.Tensor:
     """``[1, heads, total_queries, dim]`` in, the same out; the kernel works token-first."""
     from liteinfer_amd.paged_kernels import paged_prefill
 
-    # The host lengths, when the payload carries them, say whether the pass
-    # has one-query sequences and which kernel should take them.
+    # The host query lengths, when the payload carries them, say whether the
+    # pass has one-query sequences (None: the kernels find out on the device).
     one_query_rows = None
-    if kv.host_query_lens and kv.host_context_lens:
-        one_query_rows = _one_query_rows_to_decode_kernel(
-            kv.host_query_lens, kv.host_context_lens, query.shape[1], kv.key_pool.shape[1], query.shape[-1],
-            kv.key_pool.element_size())
+    if kv.host_query_lens:
+        one_query_rows = _one_query_rows_to_decode_kernel(kv.host_query_lens)
     out = paged_prefill(
         query.squeeze(0).transpose(0, 1), kv.key_pool, kv.value_pool, kv.slot_table, kv.context_lens,
         kv.query_start_loc, kv.max_query_len, scaling, num_kv_groups, one_query_rows=one_query_rows,

@@ -44,7 +44,9 @@ struct AttnArgs {
   int part_heads;  // balanced decode: KV heads per partial slot (1; kDecodeHeadGroup when head-grouped)
   int seg_cost;    // head-grouped decode: work units charged per segment start, on top of its 32-key tiles
   int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
-  int* queue;    // MFMA prefill: kPrefillQueues unit counters, then the number of blocks listed in `work`
+  int* queue;    // MFMA prefill: kPrefillQueues unit counters, the number of blocks listed in `work`, then
+                 // (prefill_pp_rows) the number of work-groups that fold the one-query rows first
+  int row_groups_max;  // prefill_pp_rows: work-groups of its grid (0: the one-query rows are not in the launch)
   // fp8 (e4m3) pools: kp / vp hold K / k_scale and V / v_scale, one byte per
   // element (pool strides in bytes); the MFMA kernels only. Other pools hold
   // the query's dtype and ignore the scales.
@@ -79,6 +81,13 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s);
 // MFMA prefill: same applicability rules as decode.
 bool prefill_mfma_applies(const AttnArgs& a, int dtype);
 int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t s);
+// A packed pass over a 16-bit pool whose one-query rows (the balanced decode
+// split, `d`: part_heads 1, its workspace set) share the prefill launch: the
+// first work-groups fold the rows, then join the chunks' queues; the rows'
+// pieces are combined after. `a` as for launch_prefill_mfma.
+int launch_prefill_with_rows(const AttnArgs& a, const AttnArgs& d, int dtype, hipStream_t s);
+// The combine of the balanced split's pieces (decode_mfma.hip).
+int launch_combine_balanced(const AttnArgs& d, int dtype, hipStream_t s);
 // Entries of the MFMA prefill work list for a pass over a slot table
 // max_context wide: an upper bound on its query blocks.
 size_t prefill_work_entries(int batch, int max_context);

@@ -366,7 +366,7 @@ extern "C" int li_paged_decode_noalloc(const void* q, int64_t q_stride_seq, int6
 // for the one-query sequences, then the prefill work list and its queues.
 size_t prefill_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads, int max_context) {
   return balanced_workspace(waves, groups, head_dim, batch, num_kv_heads) +
-         align256(prefill_work_entries(batch, max_context) * sizeof(int)) + align256((kPrefillQueues + 1) * sizeof(int));
+         align256(prefill_work_entries(batch, max_context) * sizeof(int)) + align256((kPrefillQueues + 2) * sizeof(int));
 }
 
 extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,
@@ -453,6 +453,12 @@ int paged_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
     d.block_q = 1;
     d.num_qblocks = 1;
     set_balanced(d, waves, workspace);
+    if (!a.kv_fp8 && max_query_len > 1) {
+      // Chunks and rows in one launch (16-bit pools): the rows' work-groups
+      // run the per-head split, which fits the prefill kernel's registers.
+      d.part_heads = 1;
+      return launch_prefill_with_rows(a, d, dtype, s);
+    }
     if (int rc = launch_decode_mfma(d, dtype, s)) return rc;
     if (max_query_len <= 1) return LI_OK;
     a.single_query_elsewhere = 1;

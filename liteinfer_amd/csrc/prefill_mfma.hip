@@ -51,6 +51,7 @@
 // 8 there is one queue per XCD (work-group i runs on XCD i % 8) holding the
 // KV heads q, q + 8, ...: every block of one KV head is folded on one XCD and
 // reuses that head's K/V from the XCD's L2.
+#include "decode_wave.h"
 #include "li_attention.h"
 #include "li_mfma.h"
 
@@ -531,8 +532,57 @@ constexpr int kSlotHalfStages = kSlotRing / 2 / kStageKeys;
 // other wave's vector work leaves the matrix core idle.
 constexpr int kPpMatrixPriority = 2;
 
-template <typename T, int D>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp(AttnArgs a) {
+// LDS of one ping-pong work-group: the K and V rows of each ring stage, the
+// slot ring, and the unit being folded (claimed, and its output rows).
+template <int D>
+struct PpLds {
+  static constexpr int kRegion = 2 * 32 * TileLayout<D>::kRowBytes;  // a stage's K (or V) rows
+  __attribute__((aligned(16))) int sl[kSlotRing];
+  __attribute__((aligned(1024))) char kst[kPpRing][kRegion];
+  __attribute__((aligned(1024))) char vst[kPpRing][kRegion];
+  int unit;
+  int rows[3];  // the unit's first token + q0, its query count, first head
+};
+
+// Waves of a prefill_pp_rows work-group that fold one-query rows (the LDS
+// of four decode waves matches the ping-pong work-group's).
+constexpr int kRowWaves = 4;
+// Flops of chunk work per byte of row K/V that put the rows' end at about
+// three quarters of the chunks' (prefill_order's split): a CU of the
+// ping-pong kernel folds ~4.3 TFLOP/s of causal pairs (C3-like chunks,
+// ~44% of the bf16 peak over 256 CUs), and a work-group of four decode waves
+// streams ~36 GB/s beside the chunks' work-groups (both measured on MI355X:
+// config 3's step is flat at 307 us from 48 to 80 row work-groups and
+// rises to 340 / 407 us at 40 / 32), so the rows need B / 36e9 s of one CU
+// for every F / 4.3e12 s of chunks: 4.3e12 / (0.75 * 36e9) ~ 160.
+constexpr double kRowFlopsPerByte = 160.0;
+
+// LDS of a ping-pong work-group; prefill_pp_rows's row waves use it first.
+template <int D>
+union PpShared {
+  PpLds<D> pp;
+  DecodeLds<D, false> rows[kRowWaves];
+};
+
+// The ping-pong work of work-group blockIdx.x of the persistent grid (its
+// queue: blockIdx.x % kPrefillQueues). With kRows (prefill_pp_rows), the
+// first work-groups fold the pass's one-query rows first (the balanced
+// decode split, AttnArgs `d`, over kRowWaves waves of each of them; their
+// count was written by prefill_order), then join the queues.
+template <typename T, int D, bool kRows>
+__device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
+  __shared__ __attribute__((aligned(1024))) PpShared<D> lds;
+  const unsigned wg = blockIdx.x;
+  if constexpr (kRows) {
+    const int row_groups = __builtin_amdgcn_readfirstlane(a.queue[kPrefillQueues + 1]);
+    if ((int)wg < row_groups) {
+      const int rw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+      if (rw < kRowWaves)
+        decode_balanced_wave<T, D, false>(d, (int)wg * kRowWaves + rw, (int64_t)row_groups * kRowWaves, lds.rows[rw]);
+      // (Every row wave's loads have landed: its folds consumed them.)
+      __syncthreads();
+    }
+  }
   constexpr int W = 8;
   using M = Mfma<T>;
   using Frag = typename M::Frag;
@@ -543,9 +593,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int kHalf = 32 * L::kRowBytes;  // one 32-key tile's K (or V) rows
   constexpr int kRegion = 2 * kHalf;          // a stage's K (or V) rows
   static_assert(kPpRing == 4, "the loop body covers four stages");
-  __shared__ __attribute__((aligned(16))) int sl[kSlotRing];
-  __shared__ __attribute__((aligned(1024))) char kst[kPpRing][kRegion];  // K rows of each stage
-  __shared__ __attribute__((aligned(1024))) char vst[kPpRing][kRegion];  // V rows of each stage
+  static_assert(kRegion == PpLds<D>::kRegion, "one stage region size");
+  auto& sl = lds.pp.sl;
+  auto& kst = lds.pp.kst;  // K rows of each stage
+  auto& vst = lds.pp.vst;  // V rows of each stage
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -554,13 +605,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int n = lane & 15, g = lane >> 4;
 
   const int nqueues = a.num_kv_heads % kPrefillQueues == 0 ? kPrefillQueues : 1;
-  const int qi = blockIdx.x % nqueues;
+  const int qi = (int)(wg % (unsigned)nqueues);
   const int heads_per_queue = a.num_kv_heads / nqueues;
   const int units = a.queue[kPrefillQueues] * heads_per_queue;
   // Work-group barriers here order LDS only (lds_barrier): a unit's output
   // stores and the loads in flight never hold a barrier up.
-  __shared__ int s_unit;
-  __shared__ int s_rows[3];  // the unit's first token + q0, its query count, first head
+  int& s_unit = lds.pp.unit;
+  auto& s_rows = lds.pp.rows;
   if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
   int next_unit = 0;  // tid 0: the unit claimed for after this one
   for (;;) {
@@ -972,6 +1023,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }  // units
 }
 
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp(AttnArgs a) {
+  prefill_pp_body<T, D, false>(a, a);
+}
+
+// A packed pass's chunks and one-query rows in one launch: the first
+// work-groups fold the rows (the balanced decode split `d`, kRowWaves waves
+// each), while the others start on the chunks; each joins the chunks'
+// queues when its rows are done. The rows stream K/V from HBM while the
+// chunks keep the matrix cores busy, instead of one waiting for the other.
+template <typename T, int D>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp_rows(AttnArgs a,
+                                                                                                  AttnArgs d) {
+  prefill_pp_body<T, D, true>(a, d);
+}
+
 // Work list of the prefill grid: every non-empty query block
 // (sequence * num_qblocks + block), a sequence's blocks side by side, last
 // (heaviest) block first, the sequences ordered by the 32-key tiles of their
@@ -989,6 +1056,7 @@ constexpr int kOrderBins = 256;
 __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   __shared__ int hist[kOrderBins];
   __shared__ int max_tiles;
+  __shared__ unsigned long long row_keys, chunk_pairs;  // prefill_pp_rows's balance
   const int tid = threadIdx.x;
   // Blocks of sequence `seq` the prefill folds, and the tiles of its
   // heaviest (last) block.
@@ -1005,7 +1073,11 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   int c_t = 0;
   const int c_nb = tid < a.batch ? blocks_of(tid, &c_t) : 0;
   if (tid < kOrderBins) hist[tid] = 0;
-  if (tid == 0) max_tiles = 0;
+  if (tid == 0) {
+    max_tiles = 0;
+    row_keys = 0;
+    chunk_pairs = 0;
+  }
   __syncthreads();
   int local = c_t;
   for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
@@ -1068,6 +1140,46 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   // The persistent grid's queues start empty for this launch.
   if (tid < kPrefillQueues) a.queue[tid] = 0;
   if (tid == 0) a.queue[kPrefillQueues] = max_tiles;
+  if (a.row_groups_max > 0) {
+    // prefill_pp_rows: how many work-groups fold the one-query rows first.
+    // The rows' K/V bytes against the chunks' flops (visible causal pairs),
+    // scaled by kRowFlopsPerByte: the rows then finish about when three
+    // quarters of the chunks' work is done, and their work-groups take
+    // chunk units for the rest. A multiple of the queue count, so every
+    // XCD gives the rows the same number of CUs.
+    int64_t keys = 0, pairs = 0;
+    for (int sq = tid; sq < a.batch; sq += 1024) {
+      const int nq = a.qsl[sq + 1] - a.qsl[sq];
+      const int c = max(a.ctx[sq], 0);
+      if (nq == 1) keys += c;
+      else if (nq > 1) pairs += (int64_t)nq * max(c - nq, 0) + (int64_t)nq * (nq + 1) / 2;
+    }
+    keys = wave_sum_i64(keys);
+    pairs = wave_sum_i64(pairs);
+    if ((tid & 63) == 0) {
+      atomicAdd(&row_keys, (unsigned long long)keys);
+      atomicAdd(&chunk_pairs, (unsigned long long)pairs);
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const int g = a.row_groups_max;
+      int groups = 0;
+      if (row_keys > 0 && chunk_pairs == 0) {
+        groups = g;
+      } else if (row_keys > 0) {
+        const double bytes = (double)row_keys * 2.0 * a.num_kv_heads * a.head_dim * 2.0;
+        const double flops = (double)chunk_pairs * 4.0 * a.num_heads * a.head_dim;
+        const double want = g * kRowFlopsPerByte * bytes / flops;
+        // At most what leaves a work-group for each chunk unit, up to half
+        // the grid: the chunks' units all start at once when they are few.
+        const int units = max_tiles * a.num_kv_heads;
+        const int keep = min((units + kPrefillQueues - 1) / kPrefillQueues, g / 2 / kPrefillQueues) * kPrefillQueues;
+        groups = (int)(want / kPrefillQueues + 0.5) * kPrefillQueues;
+        groups = max(kPrefillQueues, min(groups, g - max(keep, kPrefillQueues)));
+      }
+      a.queue[kPrefillQueues + 1] = groups;
+    }
+  }
 }
 
 bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
@@ -1092,23 +1204,37 @@ bool prefill_mfma_applies(const AttnArgs& a, int dtype) {
          rows_aligned(a.kp, a.p_s0, a.p_s1, pe) && rows_aligned(a.vp, a.p_s0, a.p_s1, pe);
 }
 
+// `rows`: the one-query rows' decode split to run in the same launch
+// (prefill_pp_rows), or null.
 template <int W>
-static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
+static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const AttnArgs* rows) {
   a.block_q = 32 * W / a.groups;
   a.num_qblocks = cdiv(a.max_query_len, a.block_q);
   const int64_t units = (int64_t)a.batch * a.num_kv_heads * a.num_qblocks;
   if (units == 0) return LI_OK;
   if ((size_t)a.batch * a.num_qblocks > prefill_work_entries(a.batch, a.max_context))
     return fail(LI_EINVAL, "prefill: %d query blocks per sequence exceed the planned work list", a.num_qblocks);
-  hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
-  if (int rc = check_launch("prefill_order")) return rc;
   // One work-group per CU (its LDS and registers fill one), a multiple of
   // the queue count so every queue has work-groups, and never more than
-  // there can be units.
+  // there can be units (the rows' work-groups aside).
   int64_t grid = (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues;
-  grid = std::min<int64_t>(grid, (units + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues);
+  if (!rows) grid = std::min<int64_t>(grid, (units + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues);
+  a.row_groups_max = rows ? (int)grid : 0;
+  hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
+  if (int rc = check_launch("prefill_order")) return rc;
   const dim3 block(64 * W);
   const dim3 g((unsigned)grid);
+  if (rows) {
+    if (dtype == LI_BF16) {
+      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp_rows<li_bf16, 128>), g, block, 0, s, a, *rows);
+      else hipLaunchKernelGGL((prefill_pp_rows<li_bf16, 64>), g, block, 0, s, a, *rows);
+    } else {
+      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp_rows<li_f16, 128>), g, block, 0, s, a, *rows);
+      else hipLaunchKernelGGL((prefill_pp_rows<li_f16, 64>), g, block, 0, s, a, *rows);
+    }
+    if (int rc = check_launch("prefill_pp_rows")) return rc;
+    return launch_combine_balanced(*rows, dtype, s);
+  }
   if (a.kv_fp8) {
     if (dtype == LI_BF16) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true>), g, block, 0, s, a);
     else hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true>), g, block, 0, s, a);
@@ -1122,7 +1248,17 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s) {
   return check_launch("prefill_mfma");
 }
 
-int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) { return launch_prefill_waves<kWaves>(in, dtype, s); }
+int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) {
+  return launch_prefill_waves<kWaves>(in, dtype, s, nullptr);
+}
+
+int launch_prefill_with_rows(const AttnArgs& in, const AttnArgs& d, int dtype, hipStream_t s) {
+  if (in.kv_fp8 || d.part_heads != 1 || !d.part_o)
+    return fail(LI_EINVAL, "prefill with rows: 16-bit pools and a per-head decode split only");
+  AttnArgs a = in;
+  a.single_query_elsewhere = 1;
+  return launch_prefill_waves<kWaves>(a, dtype, s, &d);
+}
 
 
 }  // namespace li

@@ -163,3 +163,34 @@ def test_a_packed_pass_writes_its_rows_and_nothing_around_them(one_query_rows, p
     if pool == "bf16":
         assert_within(got, b.oracle(), 2 ** -6, 2e-3)
     assert torch.isfinite(got.float()).all()
+
+
+_RNG = np.random.default_rng(11)
+_MANY_ROWS = _RNG.integers(200, 3000, size=160).tolist()
+
+
+@pytest.mark.parametrize(
+    ("contexts", "query_lens"),
+    [
+        ([700] + _MANY_ROWS, [300] + [1] * len(_MANY_ROWS)),
+        ([2100, 1500, 1800, 999], [2000, 1500, 700, 1]),
+        ([30000, 45000, 600, 2600], [1, 1, 512, 1]),
+        ([5000, 77, 1], [1, 77, 1]),
+    ],
+    ids=["rows-outweigh-one-chunk", "one-row-beside-chunks", "long-rows-in-pieces", "a-one-key-row"],
+)
+@pytest.mark.parametrize(
+    ("dtype", "head_dim", "num_heads", "num_kv_heads"),
+    [(torch.bfloat16, 128, 32, 8), (torch.float16, 64, 16, 8), (torch.bfloat16, 128, 12, 3)],
+    ids=["bf16-d128", "f16-d64", "three-kv-heads"],
+)
+def test_rows_and_chunks_share_the_prefill_launch(contexts, query_lens, dtype, head_dim, num_heads, num_kv_heads):
+    """16-bit pools: the one-query rows are folded by the prefill launch's first
+    work-groups (the decode split, as many work-groups as the rows' bytes
+    against the chunks' flops ask for), which then join the chunks' queues."""
+    b = PagedBatch(contexts, query_lens, dtype=dtype, num_heads=num_heads, num_kv_heads=num_kv_heads,
+                   head_dim=head_dim, num_slots=65536)
+    expected = b.oracle()
+    assert_within(_run(b), expected, 2 ** -6, 2e-3)
+    # Folding the rows as query blocks of the prefill instead gives the same attention.
+    assert_within(_run(b, one_query_rows=False), expected, 2 ** -6, 2e-3)
