@@ -61,12 +61,10 @@ enum li_flags {
                                runs its balanced split (the same attention,
                                within fp32 rounding of the partial combine) */
   LI_FLAG_PREFILL_ONLY = 4   /* li_paged_prefill on the MFMA path: the prefill
-                               kernel serves every sequence, one-query ones
-                               included, and the split decode kernel is not
-                               launched (for passes with no one-query
-                               sequences, or with few and short ones next to
-                               long chunks, which then fill in behind the
-                               chunks' units; correct either way) */
+                               kernel folds every sequence as query blocks,
+                               one-query ones included, and the decode split
+                               does not run (for passes with no one-query
+                               sequences; correct either way) */
 };
 
 /* Message of the last failure on this thread ("" if none). */
