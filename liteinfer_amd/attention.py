@@ -193,7 +193,9 @@ def _one_query_rows_to_decode_kernel(query_lens) -> bool:
     (``prefill_pp_rows``; config 3: 316-335 us against 341-387 us with the
     rows folded as prefill units, where each row walks its whole context
     through a 256-row work-group at matrix-core speed; no case measured
-    slower). Over an fp8 pool the decode kernel runs before the prefill.
+    slower; over an fp8 pool the lockstep prefill does the same: 359-365
+    against 412 us, and ~382 us with the rows in a decode launch of their
+    own before it).
     False (no decode launch, ``LI_FLAG_PREFILL_ONLY``) when there are none;
     a caller may still ask for the folded form with ``one_query_rows=False``.
     The answer is the same attention either way.

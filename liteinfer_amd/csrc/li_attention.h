@@ -81,8 +81,8 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s);
 // MFMA prefill: same applicability rules as decode.
 bool prefill_mfma_applies(const AttnArgs& a, int dtype);
 int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t s);
-// A packed pass over a 16-bit pool whose one-query rows (the balanced decode
-// split, `d`: part_heads 1, its workspace set) share the prefill launch: the
+// A packed pass whose one-query rows (the balanced decode split, `d`:
+// part_heads 1, its workspace set) share the prefill launch: the
 // first work-groups fold the rows, then join the chunks' queues; the rows'
 // pieces are combined after. `a` as for launch_prefill_mfma.
 int launch_prefill_with_rows(const AttnArgs& a, const AttnArgs& d, int dtype, hipStream_t s);

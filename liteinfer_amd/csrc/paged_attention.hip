@@ -453,9 +453,9 @@ int paged_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
     d.block_q = 1;
     d.num_qblocks = 1;
     set_balanced(d, waves, workspace);
-    if (!a.kv_fp8 && max_query_len > 1) {
-      // Chunks and rows in one launch (16-bit pools): the rows' work-groups
-      // run the per-head split, which fits the prefill kernel's registers.
+    if (max_query_len > 1) {
+      // Chunks and rows in one launch: the rows' work-groups run the
+      // per-head split, which fits the prefill kernels' registers.
       d.part_heads = 1;
       return launch_prefill_with_rows(a, d, dtype, s);
     }

@@ -132,10 +132,56 @@ __device__ __forceinline__ void convert_stage(uint32_t raw, uint32_t dst, int ti
   }
 }
 
+// Work-groups of a prefill launch that also serves the pass's one-query
+// rows (prefill_pp_rows, prefill_mfma_rows) fold them first: the first
+// `row_groups` work-groups (prefill_order's count) run the balanced decode
+// split `d`, kRowWaves waves each, in the LDS of their rows[] member, then
+// all of the work-group's waves meet at a barrier before the prefill work
+// reuses that LDS. The LDS of four decode waves fits in a prefill
+// work-group's.
+constexpr int kRowWaves = 4;
+
+template <typename T, int D, bool F8, typename Shared>
+__device__ __forceinline__ void fold_rows_first(const AttnArgs& a, const AttnArgs& d, Shared& lds) {
+  const int row_groups = __builtin_amdgcn_readfirstlane(a.queue[kPrefillQueues + 1]);
+  const int wg = (int)blockIdx.x;
+  if (wg < row_groups) {
+    const int rw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    if (rw < kRowWaves)
+      decode_balanced_wave<T, D, F8>(d, wg * kRowWaves + rw, (int64_t)row_groups * kRowWaves, lds.rows[rw]);
+    // (Every row wave's loads have landed: its folds consumed them.)
+    __syncthreads();
+  }
+}
+
+// Keys whose slots the lockstep kernel stages in LDS at a time (restaging
+// costs a pipeline drain, so chunks are long).
+constexpr int kLockstepChunk = 4096;
+
+// LDS of one lockstep work-group: staged slots, the converted (or, for
+// 16-bit pools, loaded) stages, an fp8 pool's raw stages, and its unit.
+template <int D, bool F8>
+struct LockstepLds {
+  __attribute__((aligned(16))) int sl[kLockstepChunk + kStageKeys];
+  __attribute__((aligned(1024))) char stages[2][2 * TileLayout<D>::kTileBytes];
+  __attribute__((aligned(1024))) char raw[F8 ? 2 : 1][F8 ? 2 * F8Tile::kTileBytes : 16];
+  int unit;
+};
+
+template <int D, bool F8>
+union LockstepShared {
+  LockstepLds<D, F8> ls;
+  DecodeLds<D, F8> rows[kRowWaves];
+};
+
 // F8: the pool is fp8 (e4m3, head_dim 128); its stages land raw and are
 // converted in LDS (convert_stage) before the fold, which is the same.
-template <typename T, int D, int W, bool F8>
-__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma(AttnArgs a) {
+// With kRows (prefill_mfma_rows) the first work-groups fold the pass's
+// one-query rows first (fold_rows_first).
+template <typename T, int D, int W, bool F8, bool kRows>
+__device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d) {
+  __shared__ __attribute__((aligned(1024))) LockstepShared<D, F8> lds;
+  if constexpr (kRows) fold_rows_first<T, D, F8>(a, d, lds);
   using M = Mfma<T>;
   using Frag = typename M::Frag;
   using L = TileLayout<D>;
@@ -143,12 +189,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   static_assert(!F8 || D == 128, "fp8 pools at head_dim 128");
   constexpr int kSteps = D / 32;
   constexpr int kDmaPerStage = 2 * (2 * LS::kInsts / W);
-  // Keys whose slots are staged in LDS at a time (restaging costs a pipeline
-  // drain, so chunks are long).
-  constexpr int kChunk = 4096;
-  __shared__ __attribute__((aligned(16))) int sl[kChunk + kStageKeys];
-  __shared__ __attribute__((aligned(1024))) char stages[2][2 * L::kTileBytes];
-  __shared__ __attribute__((aligned(1024))) char raw[F8 ? 2 : 1][F8 ? 2 * F8Tile::kTileBytes : 16];
+  constexpr int kChunk = kLockstepChunk;
+  auto& sl = lds.ls.sl;
+  auto& stages = lds.ls.stages;
+  auto& raw = lds.ls.raw;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -163,10 +207,10 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   // come in the work list's order, heaviest block first: a work-group that
   // finishes early takes the next heaviest unit left.
   const int nqueues = a.num_kv_heads % kPrefillQueues == 0 ? kPrefillQueues : 1;
-  const int qi = blockIdx.x % nqueues;
+  const int qi = (int)(blockIdx.x % (unsigned)nqueues);
   const int heads_per_queue = a.num_kv_heads / nqueues;
   const int units = a.queue[kPrefillQueues] * heads_per_queue;
-  __shared__ int s_unit;
+  int& s_unit = lds.ls.unit;
   for (;;) {
   __syncthreads();  // every wave is done with the previous unit's LDS
   if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
@@ -464,6 +508,19 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) 
   }  // units
 }
 
+template <typename T, int D, int W, bool F8>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma(AttnArgs a) {
+  prefill_mfma_body<T, D, W, F8, false>(a, a);
+}
+
+// A packed pass's chunks and one-query rows in one launch, fp8 pools (the
+// 16-bit pools' counterpart is prefill_pp_rows).
+template <typename T, int D, int W, bool F8>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_rows(AttnArgs a,
+                                                                                                    AttnArgs d) {
+  prefill_mfma_body<T, D, W, F8, true>(a, d);
+}
+
 // issue_stage into a layout that keeps the K rows of every stage in one LDS
 // region and the V rows in another (kdst / vdst: this stage's 32-key tiles
 // of K, of V, 32 rows apart), so that the per-lane read addresses of either
@@ -544,9 +601,6 @@ struct PpLds {
   int rows[3];  // the unit's first token + q0, its query count, first head
 };
 
-// Waves of a prefill_pp_rows work-group that fold one-query rows (the LDS
-// of four decode waves matches the ping-pong work-group's).
-constexpr int kRowWaves = 4;
 // Flops of chunk work per byte of row K/V that put the rows' end at about
 // three quarters of the chunks' (prefill_order's split): a CU of the
 // ping-pong kernel folds ~4.3 TFLOP/s of causal pairs (C3-like chunks,
@@ -573,16 +627,7 @@ template <typename T, int D, bool kRows>
 __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   __shared__ __attribute__((aligned(1024))) PpShared<D> lds;
   const unsigned wg = blockIdx.x;
-  if constexpr (kRows) {
-    const int row_groups = __builtin_amdgcn_readfirstlane(a.queue[kPrefillQueues + 1]);
-    if ((int)wg < row_groups) {
-      const int rw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-      if (rw < kRowWaves)
-        decode_balanced_wave<T, D, false>(d, (int)wg * kRowWaves + rw, (int64_t)row_groups * kRowWaves, lds.rows[rw]);
-      // (Every row wave's loads have landed: its folds consumed them.)
-      __syncthreads();
-    }
-  }
+  if constexpr (kRows) fold_rows_first<T, D, false>(a, d, lds);
   constexpr int W = 8;
   using M = Mfma<T>;
   using Frag = typename M::Frag;
@@ -1167,7 +1212,7 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
       if (row_keys > 0 && chunk_pairs == 0) {
         groups = g;
       } else if (row_keys > 0) {
-        const double bytes = (double)row_keys * 2.0 * a.num_kv_heads * a.head_dim * 2.0;
+        const double bytes = (double)row_keys * 2.0 * a.num_kv_heads * a.head_dim * (a.kv_fp8 ? 1.0 : 2.0);
         const double flops = (double)chunk_pairs * 4.0 * a.num_heads * a.head_dim;
         const double want = g * kRowFlopsPerByte * bytes / flops;
         // At most what leaves a work-group for each chunk unit, up to half
@@ -1224,6 +1269,12 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
   if (int rc = check_launch("prefill_order")) return rc;
   const dim3 block(64 * W);
   const dim3 g((unsigned)grid);
+  if (rows && a.kv_fp8) {
+    if (dtype == LI_BF16) hipLaunchKernelGGL((prefill_mfma_rows<li_bf16, 128, W, true>), g, block, 0, s, a, *rows);
+    else hipLaunchKernelGGL((prefill_mfma_rows<li_f16, 128, W, true>), g, block, 0, s, a, *rows);
+    if (int rc = check_launch("prefill_mfma_rows")) return rc;
+    return launch_combine_balanced(*rows, dtype, s);
+  }
   if (rows) {
     if (dtype == LI_BF16) {
       if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp_rows<li_bf16, 128>), g, block, 0, s, a, *rows);
@@ -1253,8 +1304,7 @@ int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) {
 }
 
 int launch_prefill_with_rows(const AttnArgs& in, const AttnArgs& d, int dtype, hipStream_t s) {
-  if (in.kv_fp8 || d.part_heads != 1 || !d.part_o)
-    return fail(LI_EINVAL, "prefill with rows: 16-bit pools and a per-head decode split only");
+  if (d.part_heads != 1 || !d.part_o) return fail(LI_EINVAL, "prefill with rows: a per-head decode split only");
   AttnArgs a = in;
   a.single_query_elsewhere = 1;
   return launch_prefill_waves<kWaves>(a, dtype, s, &d);

@@ -441,10 +441,9 @@ def paged_prefill(
         block_kv, block_q: tiles of the general-shape kernel.
         kernel: ``"auto"`` (MFMA where it applies) or ``"generic"``.
         one_query_rows: whether any sequence brings a single query (``None``:
-            unknown). The MFMA path hands those to the balanced decode split:
-            over a 16-bit pool inside the prefill launch (its first
-            work-groups fold them, then join the chunks), over an fp8 pool
-            in a decode launch before it. ``False`` lets the prefill kernel
+            unknown). The MFMA path hands those to the balanced decode split
+            inside the prefill launch (its first work-groups fold them, then
+            join the chunks). ``False`` lets the prefill kernel
             fold every sequence as query blocks and skips the split. Either
             way the result is the same attention.
         k_scale, v_scale: the scales of an fp8 pool (see `paged_decode`).

@@ -191,6 +191,25 @@ def test_fp8_prefill_matches_the_oracle_over_dequantised_rows(q_dtype, k_scale, 
     assert_within(out, want, 2e-2, 2e-3)
 
 
+_MANY_ROWS = np.random.default_rng(13).integers(200, 3000, size=120).tolist()
+
+
+@pytest.mark.parametrize(
+    ("ctx", "q"),
+    [([700] + _MANY_ROWS, [300] + [1] * len(_MANY_ROWS)), ([30000, 45000, 600, 2600], [1, 1, 512, 1])],
+    ids=["rows-outweigh-one-chunk", "long-rows-in-pieces"],
+)
+def test_fp8_rows_and_chunks_share_the_prefill_launch(ctx, q):
+    """fp8 pools: the one-query rows run as the decode split in the lockstep
+    prefill launch's first work-groups, which then join the chunks."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    b, kp, vp, want = _fp8_packed(ctx, q, 0.05, 0.2, seed=9)
+    out = paged_prefill(b.query, kp, vp, b.slot_table, b.context_lens_t, b.query_start_loc, max(q), b.scaling,
+                        b.groups, k_scale=0.05, v_scale=0.2)
+    assert_within(out, want, 2e-2, 2e-3)
+
+
 @pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(8, 8), (16, 1), (32, 16)])
 def test_fp8_prefill_groupings(num_heads, num_kv_heads):
     from liteinfer_amd.paged_kernels import paged_prefill
