@@ -138,12 +138,17 @@ __device__ __forceinline__ void convert_stage(uint32_t raw, uint32_t dst, int ti
 // split `d`, kRowWaves waves each, in the LDS of their rows[] member, then
 // all of the work-group's waves meet at a barrier before the prefill work
 // reuses that LDS. The LDS of four decode waves fits in a prefill
-// work-group's.
+// work-group's. (Three waves with three ring stages each, two tiles in
+// flight per wave, measured no faster: config 3 flat at 310-315 us from 48
+// row work-groups.)
 constexpr int kRowWaves = 4;
 
 template <typename T, int D, bool F8, typename Shared>
 __device__ __forceinline__ void fold_rows_first(const AttnArgs& a, const AttnArgs& d, Shared& lds) {
-  const int row_groups = __builtin_amdgcn_readfirstlane(a.queue[kPrefillQueues + 1]);
+  // prefill_order's count, held to what exists: every planned row wave is a
+  // wave of the grid and has partial slots in the workspace (d.num_parts).
+  const int row_groups = min(min(__builtin_amdgcn_readfirstlane(a.queue[kPrefillQueues + 1]), (int)gridDim.x),
+                             d.num_parts / kRowWaves);
   const int wg = (int)blockIdx.x;
   if (wg < row_groups) {
     const int rw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
