@@ -252,7 +252,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
 // together.
 template <typename T>
 __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
-  constexpr int kMaxC = kMfmaMaxHeadDim / 64;  // dims per lane
+  static_assert(kMfmaMaxHeadDim <= 128, "two dims per lane in the many-piece rounds");
   constexpr int kBatch = 8;
   constexpr int kWide = 32;
   const int lane = threadIdx.x;
@@ -291,6 +291,7 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   if (n <= kBatch) {
     // At most kBatch pieces (the usual case): every piece's LSE and partial
     // row load at once, so the fold waits for one round trip, not two.
+    constexpr int kMaxC = kMfmaMaxHeadDim / 64;  // dims per lane
     const float lse = lane < n ? a.part_lse[row_of(lane)] : -INFINITY;
     float v[kBatch][kMaxC];
 #pragma unroll
@@ -325,43 +326,41 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   // More pieces (long contexts over few sequences): rounds of kWide
   // pieces, each round's LSEs and partial rows loaded together (one round
   // trip per round) and folded into a running maximum, sum and row,
-  // rescaled when the maximum grows.
+  // rescaled when the maximum grows. Lane l holds dims 2l and 2l + 1
+  // (head_dim <= 128): one 8-byte load per piece keeps a round's kWide loads
+  // within what one wave can have in flight (config 4's combine: 10.1 ->
+  // 9.3 us against one 4-byte load per dim; with at most eight pieces the
+  // 4-byte loads measured no slower, so that path keeps them).
+  const int d0 = 2 * lane;
+  const bool has = d0 < D;
+  auto piece = [&](int j) -> float2 {
+    return has ? *reinterpret_cast<const float2*>(a.part_o + row_of(j) * D + d0) : float2{0.f, 0.f};
+  };
   float m = -INFINITY, wsum = 0.f;
-  float acc[kMaxC];
-#pragma unroll
-  for (int c = 0; c < kMaxC; ++c) acc[c] = 0.f;
+  float2 acc = {0.f, 0.f};
   for (int j0 = 0; j0 < n; j0 += kWide) {
     const int jn = min(kWide, n - j0);
     const float lse = lane < jn ? a.part_lse[row_of(j0 + lane)] : -INFINITY;
-    float v[kWide][kMaxC];
+    float2 v[kWide];
 #pragma unroll
-    for (int k = 0; k < kWide; ++k) {
-      const float* po = a.part_o + row_of(j0 + min(k, jn - 1)) * D;
-#pragma unroll
-      for (int c = 0; c < kMaxC; ++c) {
-        const int d = lane + 64 * c;
-        v[k][c] = (k < jn && d < D) ? po[d] : 0.f;
-      }
-    }
+    for (int k = 0; k < kWide; ++k) v[k] = piece(j0 + min(k, jn - 1));
     const float nm = fmaxf(m, li_wave_max(lse));
     const float keep = m == -INFINITY ? 0.f : exp2f(m - nm);
     const float wl = lane < jn ? exp2f(lse - nm) : 0.f;
     wsum = wsum * keep + li_wave_sum(wl);
-#pragma unroll
-    for (int c = 0; c < kMaxC; ++c) acc[c] *= keep;
+    acc.x *= keep;
+    acc.y *= keep;
 #pragma unroll
     for (int k = 0; k < kWide; ++k) {
-      const float wt = __shfl(wl, k, 64);
-#pragma unroll
-      for (int c = 0; c < kMaxC; ++c) acc[c] = fmaf(wt, v[k][c], acc[c]);
+      const float wt = k < jn ? __shfl(wl, k, 64) : 0.f;
+      acc.x = fmaf(wt, v[k].x, acc.x);
+      acc.y = fmaf(wt, v[k].y, acc.y);
     }
     m = nm;
   }
-  const float inv = 1.f / wsum;
-#pragma unroll
-  for (int c = 0; c < kMaxC; ++c) {
-    const int d = lane + 64 * c;
-    if (d < D) orow[d] = li_from_float<T>(acc[c] * inv);
+  if (has) {
+    const float inv = 1.f / wsum;
+    *reinterpret_cast<uint32_t*>(orow + d0) = li_pack2<T>(acc.x * inv, acc.y * inv);
   }
 }
 
