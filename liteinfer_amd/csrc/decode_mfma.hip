@@ -330,7 +330,8 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   // (head_dim <= 128): one 8-byte load per piece keeps a round's kWide loads
   // within what one wave can have in flight (config 4's combine: 10.1 ->
   // 9.3 us against one 4-byte load per dim; with at most eight pieces the
-  // 4-byte loads measured no slower, so that path keeps them).
+  // 4-byte loads measured faster, config 2's combine 4.3 against 4.8 us, so
+  // that path keeps them).
   const int d0 = 2 * lane;
   const bool has = d0 < D;
   auto piece = [&](int j) -> float2 {
