@@ -265,8 +265,9 @@ int li_paged_decode_noalloc(const void* q, int64_t q_stride_seq,
  * Workspace bytes li_paged_prefill needs for a pass of `batch` sequences over
  * a slot table `max_context` wide on a device of `num_cus` compute units
  * (0 = ask the current device): partials of its one-query sequences, which
- * the decode kernel serves with a partitioned key axis, and the list that
- * orders the prefill kernel's query blocks longest first. No counterpart in
+ * the decode kernel's balanced split serves with a partitioned key axis (run
+ * by the first work-groups of the prefill launch), and the list that orders
+ * the prefill kernel's query blocks longest first. No counterpart in
  * the reference, whose prefill kernel allocates nothing
  * (liteinfer/models/paged_kernels.py:867). The size is for the current
  * device (its CU count sizes the grid the launch runs); num_cus is accepted
@@ -306,7 +307,7 @@ int li_paged_prefill(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
  * li_paged_prefill over a pool of element type kv_dtype: `dtype` (then the
  * scales are ignored and this is li_paged_prefill) or LI_FP8_E4M3, as for
  * li_paged_decode_ex (its one-query sequences run on li_paged_decode_ex's
- * kernel). fp8 pools run on the MFMA kernels only (bf16 / fp16 queries,
+ * per-wave code, inside the prefill launch). fp8 pools run on the MFMA kernels only (bf16 / fp16 queries,
  * head_dim 128; otherwise LI_EUNSUPPORTED). No counterpart in the
  * reference's code (its planned quantised cache, docs/roadmap.md 2.5).
  */
