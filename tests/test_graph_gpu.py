@@ -1,4 +1,4 @@
-"""A decode step captured into a HIP graph replays correctly for changing contexts.
+"""A decode step (and a packed pass) captured into a HIP graph replays correctly for changing contexts.
 
 The reference captures its decode steps (liteinfer/engine/cuda_graphs.py:
 105-260): the slot table and context lengths are static buffers rewritten
@@ -108,4 +108,55 @@ def test_captured_grid_does_not_depend_on_contexts():
         eager = step.run()
         torch.cuda.synchronize()
         assert torch.equal(replayed, eager)
+        assert np.isfinite(replayed.float().cpu().numpy()).all()
+
+
+def test_captured_packed_pass_with_rows_matches_eager_on_every_replay():
+    """A packed pass (chunks and one-query rows in one prefill launch) captured
+    once: the rows' work-group count and the work list are computed on the
+    device on every replay, so new lengths need no new capture."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    g = torch.Generator(device=DEV).manual_seed(7)
+    batch, tokens, width, heads, kv_heads, dim, num_slots = 6, 600, 4096, 32, 8, 128, 1 << 16
+    bf = torch.bfloat16
+    key_pool = torch.randn(num_slots, kv_heads, dim, generator=g, device=DEV).to(bf)
+    value_pool = torch.randn(num_slots, kv_heads, dim, generator=g, device=DEV).to(bf)
+    query = torch.empty(tokens, heads, dim, dtype=bf, device=DEV)
+    slot_table = torch.empty(batch, width, dtype=torch.int64, device=DEV)
+    context_lens = torch.empty(batch, dtype=torch.int32, device=DEV)
+    qsl = torch.empty(batch + 1, dtype=torch.int32, device=DEV)
+    max_query_len = 400
+
+    def refill(qlens, seed):
+        gg = torch.Generator(device=DEV).manual_seed(seed)
+        assert sum(qlens) == tokens and max(qlens) <= max_query_len
+        ctx = [q + int(torch.randint(0, width - q + 1, (1,), generator=gg, device=DEV)) for q in qlens]
+        context_lens.copy_(torch.tensor(ctx, dtype=torch.int32))
+        qsl.copy_(torch.tensor([0, *np.cumsum(qlens).tolist()], dtype=torch.int32))
+        slot_table.copy_(torch.randint(0, num_slots, (batch, width), generator=gg, device=DEV))
+        query.copy_(torch.randn(query.shape, generator=gg, device=DEV).to(bf))
+
+    def run():
+        return paged_prefill(query, key_pool, value_pool, slot_table, context_lens, qsl, max_query_len,
+                             dim ** -0.5, heads // kv_heads)
+
+    refill([400, 100, 97, 1, 1, 1], 0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+    for i, qlens in enumerate(([400, 100, 97, 1, 1, 1], [300, 296, 1, 1, 1, 1], [1, 1, 1, 1, 196, 400],
+                               [200, 200, 197, 1, 1, 1], [100, 100, 100, 100, 100, 100])):
+        refill(qlens, 10 + i)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out.clone()
+        eager = run()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), qlens
         assert np.isfinite(replayed.float().cpu().numpy()).all()
