@@ -126,6 +126,48 @@ struct DecodeState {
 // operands meet dim for dim.
 typedef int v8i_t __attribute__((ext_vector_type(8)));
 
+// Splits one row of the query into e4m3 terms for the fp8 score MFMAs: the
+// lane holds 32 of the row's values (x, dims 32 g ..), the row's four lanes
+// (same n) together the whole row. The row is scaled by the exact power of
+// two 2^e that puts its largest |value| in [128, 256), then each term is the
+// e4m3 rounding of what the terms before it left (byte i of the lane's term
+// is its value i). Returns 2^-e, which takes the scores back to the query's
+// units.
+template <int kTerms>
+__device__ __forceinline__ float split_e4m3(float (&x)[32], v8i_t (&t)[kTerms]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  amax = li_group_max(amax);  // the row's four lanes
+  // amax in [2^(E-127), 2^(E-126)): 2^(134-E) puts it in [2^7, 2^8).
+  const int ex = min(max(134 - (int)((__float_as_uint(amax) >> 23) & 0xff), -126), 126);
+  const float mult = __uint_as_float((uint32_t)(127 + ex) << 23);
+#pragma unroll
+  for (int i = 0; i < 32; ++i) x[i] *= mult;
+  typedef short s2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int tt = 0; tt < kTerms; ++tt) {
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      s2_t b = {0, 0};
+      b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(b, x[4 * w], x[4 * w + 1], 1.f, false);
+      b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(b, x[4 * w + 2], x[4 * w + 3], 1.f, true);
+      const uint32_t bits = __builtin_bit_cast(uint32_t, b);
+      t[tt][w] = (int)bits;
+      if (tt + 1 < kTerms) {
+        // What this term left: exact in fp32.
+        const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, false);
+        const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, true);
+        x[4 * w] -= lo[0];
+        x[4 * w + 1] -= lo[1];
+        x[4 * w + 2] -= hi[0];
+        x[4 * w + 3] -= hi[1];
+      }
+    }
+  }
+  return __uint_as_float((uint32_t)(127 - ex) << 23);
+}
+
 template <typename T, int D, bool F8>
 struct DecodeQuery {
   typename Mfma<T>::Frag f[D / 32];
@@ -319,37 +361,7 @@ __device__ __forceinline__ void load_query(const AttnArgs& a, int row, int kvh, 
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)f[e];
     }
-    float amax = 0.f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = li_group_max(amax);  // the head's four lanes
-    // amax in [2^(E-127), 2^(E-126)): 2^(134-E) puts it in [2^7, 2^8).
-    const int ex = min(max(134 - (int)((__float_as_uint(amax) >> 23) & 0xff), -126), 126);
-    const float mult = __uint_as_float((uint32_t)(127 + ex) << 23);
-    q.scale = __uint_as_float((uint32_t)(127 - ex) << 23);
-#pragma unroll
-    for (int i = 0; i < 32; ++i) x[i] *= mult;
-    typedef short s2_t __attribute__((ext_vector_type(2)));
-#pragma unroll
-    for (int t = 0; t < DecodeQuery<T, D, F8>::kTerms; ++t) {
-#pragma unroll
-      for (int w = 0; w < 8; ++w) {
-        s2_t b = {0, 0};
-        b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(b, x[4 * w], x[4 * w + 1], 1.f, false);
-        b = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(b, x[4 * w + 2], x[4 * w + 3], 1.f, true);
-        const uint32_t bits = __builtin_bit_cast(uint32_t, b);
-        q.t[t][w] = (int)bits;
-        if (t + 1 < DecodeQuery<T, D, F8>::kTerms) {
-          // What this term left: exact in fp32.
-          const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, false);
-          const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, true);
-          x[4 * w] -= lo[0];
-          x[4 * w + 1] -= lo[1];
-          x[4 * w + 2] -= hi[0];
-          x[4 * w + 3] -= hi[1];
-        }
-      }
-    }
+    q.scale = split_e4m3<DecodeQuery<T, D, F8>::kTerms>(x, q.t);
   }
 }
 
