@@ -113,13 +113,10 @@ struct DecodeState {
 //
 // fp8 pools: the scores run on v_mfma_scale_f32_16x16x128_f8f6f4 with K
 // straight from the pool bytes (no conversion of K), so the query is given
-// in e4m3 as well: head n's row is scaled by an exact power of two 2^e that
-// puts its largest |value| in [128, 256), then split into kTerms e4m3 terms,
-// each the rounding of what the terms before it left. A bf16 value has 8
-// significant bits and an fp16 value 11; two (three) 4-bit terms hold them
-// exactly, except for values below the e4m3 normal range (2^-6, i.e. under
-// 2^-13 of the row's largest), whose last term keeps them to within 2^-10
-// -- 2^-17 of the largest. The terms' MFMAs chain into one accumulator and
+// in e4m3 as well: head n's row split into kTerms e4m3 terms by split_e4m3
+// below (a power of two per row, then terms with block scales 2^0, 2^-4,
+// 2^-8: exact for a bf16 (two terms) or fp16 (three) value down to 2^-13 of
+// the row's largest). The terms' MFMAs chain into one accumulator and
 // `scale` (2^-e) returns the scores to the query's units. Lane (n, g) holds
 // dims 32 g .. 32 g + 31 of head n, byte i of each term being dim 32 g + i,
 // the same order in which it reads the K bytes of its key, so the two
@@ -129,10 +126,17 @@ typedef int v8i_t __attribute__((ext_vector_type(8)));
 // Splits one row of the query into e4m3 terms for the fp8 score MFMAs: the
 // lane holds 32 of the row's values (x, dims 32 g ..), the row's four lanes
 // (same n) together the whole row. The row is scaled by the exact power of
-// two 2^e that puts its largest |value| in [128, 256), then each term is the
-// e4m3 rounding of what the terms before it left (byte i of the lane's term
-// is its value i). Returns 2^-e, which takes the scores back to the query's
-// units.
+// two 2^e that puts its largest |value| in [128, 256); term t is the e4m3
+// rounding of 16^t times what the terms before it left (byte i of the lane's
+// term is its value i), and its MFMA takes it with block scale 2^-4t
+// (kTermScale). Scaling each residual up keeps it in e4m3's normal range
+// (a residual is at most 2^-4 of the value it rounds, so 16 times it stays
+// under 448 and above 2^-6 whenever the value is): two terms hold a bf16
+// value's 8 significant bits exactly, three an fp16 value's 11, down to
+// values of 2^-6 after the scaling (2^-13 of the row's largest). Returns
+// 2^-e, which takes the scores back to the query's units.
+__device__ __forceinline__ constexpr int kTermScale(int t) { return 127 - 4 * t; }  // e8m0 of 2^-4t
+
 template <int kTerms>
 __device__ __forceinline__ float split_e4m3(float (&x)[32], v8i_t (&t)[kTerms]) {
   float amax = 0.f;
@@ -155,13 +159,14 @@ __device__ __forceinline__ float split_e4m3(float (&x)[32], v8i_t (&t)[kTerms]) 
       const uint32_t bits = __builtin_bit_cast(uint32_t, b);
       t[tt][w] = (int)bits;
       if (tt + 1 < kTerms) {
-        // What this term left: exact in fp32.
+        // What this term left, times 16 (exact in fp32): the next term is
+        // that, its MFMA's block scale 2^-4 taking it back.
         const auto lo = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, false);
         const auto hi = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(bits, 1.f, true);
-        x[4 * w] -= lo[0];
-        x[4 * w + 1] -= lo[1];
-        x[4 * w + 2] -= hi[0];
-        x[4 * w + 3] -= hi[1];
+        x[4 * w] = (x[4 * w] - lo[0]) * 16.f;
+        x[4 * w + 1] = (x[4 * w + 1] - lo[1]) * 16.f;
+        x[4 * w + 2] = (x[4 * w + 2] - hi[0]) * 16.f;
+        x[4 * w + 3] = (x[4 * w + 3] - hi[1]) * 16.f;
       }
     }
   }
@@ -234,9 +239,10 @@ __device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const 
     const v8i_t k0 = krow(stage), k1 = krow(stage + L::kRow16);
 #pragma unroll
     for (int t = 0; t < DecodeQuery<T, D, F8>::kTerms; ++t) {
-      // Formats e4m3 (0) for both operands, block scales 2^0 (e8m0 127).
-      s0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k0, q.t[t], s0, 0, 0, 0, 127, 0, 127);
-      s1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k1, q.t[t], s1, 0, 0, 0, 127, 0, 127);
+      // Formats e4m3 (0) for both operands; block scales 2^0 for K, 2^-4t
+      // for query term t.
+      s0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k0, q.t[t], s0, 0, 0, 0, 127, 0, kTermScale(t));
+      s1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(k1, q.t[t], s1, 0, 0, 0, 127, 0, kTermScale(t));
     }
   } else {
 #pragma unroll

@@ -108,27 +108,27 @@ __device__ __forceinline__ void issue_stage(uint32_t stage, const char* __restri
   }
 }
 
-// The V rows of an fp8 stage (raw, F8Tile layout, two 32-key tiles) into
-// the 16-bit stage the P V MFMAs read (TileLayout<128>, V half): each
-// 16-byte chunk of 16 e4m3 values of a key becomes its two 16-byte chunks of
-// bf16 / fp16, with the V swizzle. Every thread of the work-group converts
-// its share, so each value is converted once for all the waves that fold it.
-// (K is not converted: the scores run on the fp8 matrix cores with K as
-// stored.)
+// An fp8 stage (raw, F8Tile layout, two 32-key tiles) into the 16-bit stage
+// the fold reads (TileLayout<128>): each 16-byte chunk of 16 e4m3 values of
+// a key becomes its two 16-byte chunks of bf16 / fp16, K and V rows with
+// their own swizzles. Every thread of the work-group converts its share, so
+// each value is converted once for all the waves that fold it.
 template <typename T, int W>
-__device__ __forceinline__ void convert_stage_v(uint32_t raw, uint32_t dst, int tid) {
+__device__ __forceinline__ void convert_stage(uint32_t raw, uint32_t dst, int tid) {
   using Frag = typename Mfma<T>::Frag;
   using L = TileLayout<128>;
   typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 #pragma unroll
-  for (int u = tid; u < 512; u += 64 * W) {
-    const int tile = u >> 8, key = (u >> 3) & 31, c8 = u & 7;
-    const uint32_t src = raw + tile * F8Tile::kTileBytes + 32 * F8Tile::kRowBytes + F8Tile::voffset(key, c8);
+  for (int u = tid; u < 1024; u += 64 * W) {
+    const int tile = u >> 9, kv = (u >> 8) & 1, key = (u >> 3) & 31, c8 = u & 7;
+    const uint32_t src = raw + tile * F8Tile::kTileBytes + kv * 32 * F8Tile::kRowBytes +
+                         (kv ? F8Tile::voffset(key, c8) : F8Tile::offset(key, c8));
     const u4 x = *(const __attribute__((address_space(3))) u4*)(uintptr_t)src;
-    const uint32_t d = dst + tile * L::kTileBytes + 32 * L::kRowBytes;
-    *(__attribute__((address_space(3))) Frag*)(uintptr_t)(d + L::voffset(key, 2 * c8)) = f8x8_to_frag<Frag>(x[0], x[1]);
-    *(__attribute__((address_space(3))) Frag*)(uintptr_t)(d + L::voffset(key, 2 * c8 + 1)) =
-        f8x8_to_frag<Frag>(x[2], x[3]);
+    const uint32_t d = dst + tile * L::kTileBytes + kv * 32 * L::kRowBytes;
+    const uint32_t lo = d + (kv ? L::voffset(key, 2 * c8) : L::offset(key, 2 * c8));
+    const uint32_t hi = d + (kv ? L::voffset(key, 2 * c8 + 1) : L::offset(key, 2 * c8 + 1));
+    *(__attribute__((address_space(3))) Frag*)(uintptr_t)lo = f8x8_to_frag<Frag>(x[0], x[1]);
+    *(__attribute__((address_space(3))) Frag*)(uintptr_t)hi = f8x8_to_frag<Frag>(x[2], x[3]);
   }
 }
 
@@ -242,19 +242,11 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
   const int kend = pos0 + q1;  // keys this block reads: [0, kend)
   const int G = a.groups;
 
-  // This lane's two rows (one per 16-row block). 16-bit pools: the query as
-  // the 16x16x32 MFMAs take it (dims 32 j + 8 g .. of fragment j). fp8
-  // pools: the scores run on v_mfma_scale_f32_16x16x128_f8f6f4 with K as
-  // stored, the query split into e4m3 terms (split_e4m3; dims 32 g .. of the
-  // row, the order in which the lane reads its key's K bytes), each row's
-  // power of two qs[nb] returning in its softmax scale.
-  constexpr int kQTerms = !F8 ? 1 : std::is_same<T, li_f16>::value ? 3 : 2;
+  // This lane's two rows (one per 16-row block).
   int pos[2];
   bool real[2];
   int tok[2], head[2];
   Frag qf[2][kSteps];
-  v8i_t q8[2][kQTerms];
-  float qs[2] = {1.f, 1.f};
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int row = 32 * w + 16 * nb + n;
@@ -263,24 +255,13 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
     pos[nb] = real[nb] ? pos0 + q0 + ql : kend;
     tok[nb] = first_tok + q0 + ql;
     head[nb] = kvh * G + row % G;
-    const T* qrow = static_cast<const T*>(a.q) + (int64_t)tok[nb] * a.q_s0 + (int64_t)head[nb] * a.q_s1;
-    if constexpr (F8) {
-      float x[32];
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)tok[nb] * a.q_s0 + (int64_t)head[nb] * a.q_s1 + 8 * g;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const Frag f = real[nb] ? *reinterpret_cast<const Frag*>(qrow + 32 * g + 8 * i) : Frag{};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[8 * i + e] = (float)f[e];
-      }
-      qs[nb] = split_e4m3<kQTerms>(x, q8[nb]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < kSteps; ++j) {
-        if (real[nb]) {
-          qf[nb][j] = *reinterpret_cast<const Frag*>(qrow + 32 * j + 8 * g);
-        } else {
-          qf[nb][j] = Frag{};
-        }
+    for (int j = 0; j < kSteps; ++j) {
+      if (real[nb]) {
+        qf[nb][j] = *reinterpret_cast<const Frag*>(qrow + 32 * j);
+      } else {
+        qf[nb][j] = Frag{};
       }
     }
   }
@@ -302,7 +283,6 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
   // An fp8 pool stores K / k_scale and V / v_scale: the scales multiply the
   // scores and the outputs.
   const float sc = a.scale * (F8 ? a.k_scale : 1.f) * kLog2eMfma;
-  const float scn[2] = {sc * qs[0], sc * qs[1]};  // each row block's
 
   // acc[nb][blk] for blk < D / 16: dims 16 blk + 4g .. of the lane's row;
   // acc[nb][D / 16]: the row's softmax denominator, as the MFMA product of
@@ -363,32 +343,6 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
       }
     }
   };
-  // qk8 (fp8 pools): the same scores from the raw stage at `rb` (LDS byte
-  // address): lane (n, g) reads dims 32 g .. 32 g + 31 of key n (two 16-byte
-  // reads; key 16 + n sits F8Tile::kRow16 below), and the terms' MFMAs chain
-  // into one accumulator.
-  auto qk8 = [&](uint32_t rb, floatx4_t (&s)[2][4]) __attribute__((always_inline)) {
-    const uint32_t kq0 = rb + F8Tile::offset(n, 2 * g), kq1 = rb + F8Tile::offset(n, 2 * g + 1);
-    v8i_t kr[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const uint32_t tb = (b >> 1) * F8Tile::kTileBytes + (b & 1) * F8Tile::kRow16;
-      const u32x4_t lo = *(const __attribute__((address_space(3))) u32x4_t*)(uintptr_t)(kq0 + tb);
-      const u32x4_t hi = *(const __attribute__((address_space(3))) u32x4_t*)(uintptr_t)(kq1 + tb);
-      kr[b] = v8i_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-    }
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        s[nb][b] = floatx4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < kQTerms; ++t)
-          // Formats e4m3 (0) for both operands, block scales 2^0 (e8m0 127).
-          s[nb][b] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(kr[b], q8[nb][t], s[nb][b], 0, 0, 0, 127, 0,
-                                                                      127);
-      }
-  };
   // softmax: one running-max update per row block over the stage's 64 keys
   // (first key t0), the scale folded into the exponent; the weights, rounded
   // to T, into pf[nb][t] (32-key tile t), the accumulator rescaled when the
@@ -415,7 +369,7 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
         else mx = fmaxf(mx, s[nb][b][1]);
         mx = fmaxf(fmaxf(mx, s[nb][b][2]), s[nb][b][3]);
       }
-      mx = li_group_max(mx) * scn[nb];
+      mx = li_group_max(mx) * sc;
       // Lazy rescale: the running maximum only moves when the stage beats it
       // by more than kLazyRescale (log2 units), so most stages leave the
       // accumulator alone; the weights are then at most 2^kLazyRescale.
@@ -428,8 +382,8 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
         float p[8];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          p[r] = __builtin_amdgcn_exp2f(fmaf(s[nb][2 * t][r], scn[nb], -mnew));
-          p[4 + r] = __builtin_amdgcn_exp2f(fmaf(s[nb][2 * t + 1][r], scn[nb], -mnew));
+          p[r] = __builtin_amdgcn_exp2f(fmaf(s[nb][2 * t][r], sc, -mnew));
+          p[4 + r] = __builtin_amdgcn_exp2f(fmaf(s[nb][2 * t + 1][r], sc, -mnew));
         }
         u32x4_t pw;
 #pragma unroll
@@ -476,8 +430,7 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
     constexpr uint32_t sb = decltype(stage_tag)::value * 2 * L::kTileBytes;
     floatx4_t s[2][4];
     Frag pf[2][2];
-    if constexpr (F8) qk8(lds_addr(raw[decltype(stage_tag)::value]), s);
-    else qk(sb, s);
+    qk(sb, s);
     softmax(t0, s, pf);
     pv(sb, pf);
   };
@@ -518,27 +471,23 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
       }
     } else {
       // fp8: the loads fill raw[x]; after the barrier that sees them land,
-      // the work-group converts raw[x]'s V rows into stages[x], and after a
-      // second barrier the waves fold: scores from raw[x]'s K, P V from
-      // stages[x]. stages[x] is converted again only after every wave has
+      // the work-group converts raw[x] into stages[x], and after a second
+      // barrier the waves fold stages[x]. raw[x] takes its next loads once
+      // converted; stages[x] is converted again only after every wave has
       // passed the barrier of the stage in between, so after its fold.
       issue_stage<LS, W>(lds_addr(raw[0]), kpool, vpool, sl, row_bytes, 0, lane, w);
       for (int ti = 0; ti < ntiles; ti += 2) {
-        // raw[x] takes its next loads only after every wave's scores have
-        // read its K (the barrier before each issue).
-        if (ti > 0) __syncthreads();
         issue_stage<LS, W>(lds_addr(raw[1]), kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 1), kChunk), lane, w);
         li_wait_vm<kDmaPerStage>();
         __syncthreads();
-        convert_stage_v<T, W>(lds_addr(raw[0]), lds_addr(stages[0]), tid);
+        convert_stage<T, W>(lds_addr(raw[0]), lds_addr(stages[0]), tid);
         __syncthreads();
         if (!idle) fold(Stage0{}, c0 + kStageKeys * ti);
         if (ti + 1 >= ntiles) break;
-        __syncthreads();
         issue_stage<LS, W>(lds_addr(raw[0]), kpool, vpool, sl, row_bytes, min(kStageKeys * (ti + 2), kChunk), lane, w);
         li_wait_vm<kDmaPerStage>();
         __syncthreads();
-        convert_stage_v<T, W>(lds_addr(raw[1]), lds_addr(stages[1]), tid);
+        convert_stage<T, W>(lds_addr(raw[1]), lds_addr(stages[1]), tid);
         __syncthreads();
         if (!idle) fold(Stage1{}, c0 + kStageKeys * (ti + 1));
       }

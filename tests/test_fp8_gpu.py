@@ -191,6 +191,36 @@ def test_fp8_prefill_matches_the_oracle_over_dequantised_rows(q_dtype, k_scale, 
     assert_within(out, want, 2e-2, 2e-3)
 
 
+@pytest.mark.parametrize("q_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("one_query_rows", [None, False])
+def test_fp8_prefill_queries_of_any_scale(q_dtype, one_query_rows):
+    """The prefill's fp8 scores take each query row as e4m3 terms after its own power-of-two
+    scale: rows at 2^-20 .. 2^12 of the usual size, all-zero rows and rows whose elements
+    spread over 16 binades, in chunks and one-query rows, all meet the bar."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    ctx = [300, 1, 129, 700, 64]
+    q = [200, 1, 1, 31, 64]
+    b, kp, vp, _ = _fp8_packed(ctx, q, 0.5, 0.25, q_dtype=q_dtype, seed=11)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    x = b.query.float().cpu()
+    spread = torch.pow(2.0, -torch.randint(0, 17, x.shape, generator=g).float())
+    x[:, 1::4] *= spread[:, 1::4]
+    head_scale = torch.tensor([2.0 ** -20, 1.0, 2.0 ** -6, 2.0 ** 5] * (x.shape[1] // 4))
+    if q_dtype == torch.bfloat16:
+        head_scale[3::8] = 2.0 ** 12
+    x *= head_scale.view(1, -1, 1)
+    x[:, 2] = 0.0
+    b.query = x.to(q_dtype).to(DEV)
+    qsl = to_numpy(b.query_start_loc).astype(np.int32)
+    want = attend(to_numpy(b.query), fp8.dequantize(_codes(kp), 0.5), fp8.dequantize(_codes(vp), 0.25),
+                  b.slot_table.cpu().numpy(), np.asarray(ctx), b.scaling, b.groups, query_start_loc=qsl,
+                  dtype=np.float64)
+    out = paged_prefill(b.query, kp, vp, b.slot_table, b.context_lens_t, b.query_start_loc, max(q), b.scaling,
+                        b.groups, one_query_rows=one_query_rows, k_scale=0.5, v_scale=0.25)
+    assert_within(out, want, 2e-2, 2e-3)
+
+
 _MANY_ROWS = np.random.default_rng(13).integers(200, 3000, size=120).tolist()
 
 
