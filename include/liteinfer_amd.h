@@ -73,6 +73,11 @@ const char* li_last_error_string(void);
 /* Version of this ABI; bumped whenever a signature changes. */
 int li_abi_version(void);
 
+/* Digest (16 hex digits) of the csrc/ and include/ sources and the compile
+ * flags the library was built from. No counterpart in the reference: it lets
+ * a loader refuse a library built from other sources than the ones beside it. */
+const char* li_build_id(void);
+
 /*
  * KV slot-write. Replaces KVCache.scatter (liteinfer/cache/kv_cache.py:236-247)
  * together with _tokens_first (kv_cache.py:250-253):

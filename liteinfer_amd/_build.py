@@ -12,6 +12,7 @@ Run as ``python -m liteinfer_amd._build``.
 from __future__ import annotations
 
 import concurrent.futures
+import hashlib
 import os
 import shutil
 import subprocess
@@ -23,6 +24,7 @@ PACKAGE_DIR = Path(__file__).resolve().parent
 CSRC_DIR = PACKAGE_DIR / "csrc"
 LIB_DIR = PACKAGE_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libliteinfer_amd.so"
+INCLUDE_DIR = PACKAGE_DIR.parent / "include"
 
 OFFLOAD_ARCH = "gfx950"
 
@@ -49,6 +51,21 @@ SOURCE_FLAGS = {
 }
 
 
+def source_hash() -> str:
+    """16 hex digits of SHA-256 over every source and header and the compile flags.
+
+    The build passes it into the library (``li_build_id``); the loader
+    recomputes it from the files beside the package and refuses a mismatch.
+    """
+    h = hashlib.sha256()
+    files = sorted(p for p in CSRC_DIR.iterdir() if p.is_file() and p.suffix in (".hip", ".h", ".cpp"))
+    files += sorted(INCLUDE_DIR.glob("*.h"))
+    for path in files:
+        h.update(path.name.encode() + b"\0" + path.read_bytes() + b"\0")
+    h.update(repr((DEVICE_FLAGS, sorted(SOURCE_FLAGS.items()))).encode())
+    return h.hexdigest()[:16]
+
+
 def hipcc() -> str:
     rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     path = Path(rocm) / "bin" / "hipcc"
@@ -64,8 +81,9 @@ def sources() -> list[Path]:
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *DEVICE_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, build_id: str) -> None:
+    cmd = [hipcc(), *DEVICE_FLAGS, *SOURCE_FLAGS.get(src.name, []), f'-DLI_BUILD_ID="{build_id}"',
+           "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass does not know the packed-fp32 feature and says so; that
     # warning is harmless and is the only output dropped.
@@ -80,6 +98,7 @@ def _compile(src: Path, obj: Path) -> None:
 def build(verbose: bool = False) -> Path:
     """Compile every source and link the library. Always rebuilds."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
+    build_id = source_hash()
     with tempfile.TemporaryDirectory(prefix="liteinfer_amd_build_") as tmp:
         objs = []
         jobs = []
@@ -87,7 +106,7 @@ def build(verbose: bool = False) -> Path:
             for src in sources():
                 obj = Path(tmp) / (src.stem + ".o")
                 objs.append(obj)
-                jobs.append(pool.submit(_compile, src, obj))
+                jobs.append(pool.submit(_compile, src, obj, build_id))
             for job in jobs:
                 job.result()
         out_tmp = LIB_DIR / (LIB_PATH.name + ".tmp")

@@ -14,6 +14,8 @@ from pathlib import Path
 
 import torch
 
+from liteinfer_amd import _build
+
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libliteinfer_amd.so"
 
 LI_F32, LI_F16, LI_BF16, LI_FP8_E4M3 = 0, 1, 2, 3
@@ -35,6 +37,7 @@ FP8_POOL_DTYPE = torch.float8_e4m3fn
 EXPORTED_SYMBOLS = (
     "li_last_error_string",
     "li_abi_version",
+    "li_build_id",
     "li_kv_scatter",
     "li_kv_scatter_fp8",
     "li_rope_kv_write",
@@ -55,6 +58,7 @@ _i64p = ctypes.POINTER(ctypes.c_int64)
 _SIGNATURES = {
     "li_last_error_string": (ctypes.c_char_p, []),
     "li_abi_version": (_i32, []),
+    "li_build_id": (ctypes.c_char_p, []),
     "li_kv_scatter": (
         _i32,
         [_p, _p, _i64p, _i64p, _i64, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p],
@@ -107,7 +111,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -145,6 +149,13 @@ def load() -> ctypes.CDLL:
             version = lib.li_abi_version()
             if version != ABI_VERSION:
                 raise RuntimeError(f"{LIB_PATH} has ABI {version}, this package expects {ABI_VERSION}; rebuild it")
+            built = lib.li_build_id().decode()
+            expected = _build.source_hash()
+            if built != expected:
+                raise RuntimeError(
+                    f"{LIB_PATH} was built from other sources (build id {built}, the sources here hash to "
+                    f"{expected}); rebuild it with `python -m liteinfer_amd._build`"
+                )
             _lib = lib
     return _lib
 

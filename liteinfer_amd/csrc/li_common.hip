@@ -50,4 +50,12 @@ int device_cu_count() {
 
 extern "C" const char* li_last_error_string(void) { return li::g_last_error.c_str(); }
 
-extern "C" int li_abi_version(void) { return 5; }
+extern "C" int li_abi_version(void) { return 6; }
+
+// Digest of the sources and flags this library was built from, passed in by
+// the build script; the Python loader refuses a library whose digest differs
+// from the sources beside it.
+#ifndef LI_BUILD_ID
+#define LI_BUILD_ID "unknown"
+#endif
+extern "C" const char* li_build_id(void) { return LI_BUILD_ID; }

@@ -100,7 +100,7 @@ class RandomLlama:
         emb = torch.cat((freqs, freqs), dim=-1)
         return emb.cos().to(self.dtype), emb.sin().to(self.dtype)
 
-    @torch.inference_mode()
+    @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, payload,
                 logits_positions: torch.Tensor | None = None) -> torch.Tensor:
         """Logits of the selected rows.

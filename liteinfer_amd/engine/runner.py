@@ -57,7 +57,7 @@ class DecodeGraphs:
         self._pool = None
         self.captured_widths: list[int] = []
 
-    @torch.inference_mode()
+    @torch.no_grad()
     def capture_all(self) -> None:
         """Capture every width now (so no capture lands inside a timed run)."""
         for w in self.widths:
@@ -123,7 +123,7 @@ class ModelRunner:
     def release(self, seq: Sequence) -> None:
         self.cache.release(seq.request_id)
 
-    @torch.inference_mode()
+    @torch.no_grad()
     def execute(self, seqs: list[Sequence], num_tokens: list[int]) -> torch.Tensor:
         """One step over the next `num_tokens` of each sequence; logits at each one's last token."""
         ids = [s.request_id for s in seqs]

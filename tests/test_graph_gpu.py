@@ -160,3 +160,42 @@ def test_captured_packed_pass_with_rows_matches_eager_on_every_replay():
         torch.cuda.synchronize()
         assert torch.equal(replayed, eager), qlens
         assert np.isfinite(replayed.float().cpu().numpy()).all()
+
+
+def test_plain_capture_after_an_engine_capture():
+    """An engine that captured its decode graphs leaves no state that breaks a later capture.
+
+    The reference captures outside any inference-mode context
+    (liteinfer/engine/cuda_graphs.py:232-260). A capture made under
+    ``torch.inference_mode`` registers the default generator's graph state as
+    inference tensors, and every later capture outside that mode then fails in
+    ``capture_begin``; this runs both in one process, in that order.
+    """
+    from liteinfer_amd.engine.llm import LLM, EngineConfig
+    from liteinfer_amd.engine.model import LlamaShape, RandomLlama
+
+    shape = LlamaShape(hidden_size=256, num_layers=1, num_heads=4, num_kv_heads=2, head_dim=64,
+                       intermediate_size=512, vocab_size=500)
+    model = RandomLlama(shape, dtype=torch.bfloat16, seed=3, std=0.05)
+    config = EngineConfig(max_num_seqs=4, max_model_len=128, max_num_batched_tokens=64, num_gpu_blocks=64,
+                          use_graphs=True)
+    llm = LLM(model, config)
+    outputs, stats = llm.generate([[1, 2, 3, 4], [5, 6, 7]], max_tokens=4)
+    assert [len(o) for o in outputs] == [4, 4] and stats.decode_steps > 0
+    assert llm.runner.graphs.captured_widths, "the engine captured no decode graph"
+
+    step = _Step(batch=4, width=256, seed=5)
+    step.refill(0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step.run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step.run()
+    step.refill(1)
+    graph.replay()
+    torch.cuda.synchronize()
+    replayed = out.clone()
+    assert torch.equal(replayed, step.run())

@@ -8,7 +8,7 @@ from pathlib import Path
 
 import pytest
 
-from liteinfer_amd import _native
+from liteinfer_amd import _build, _native
 from liteinfer_amd.paged_kernels import _MAX_SPLITS, choose_num_splits
 
 HEADER = Path(__file__).resolve().parent.parent / "include" / "liteinfer_amd.h"
@@ -24,6 +24,22 @@ def test_library_is_built_and_loads():
     assert _native.is_built(), "run `python -m liteinfer_amd._build` (or __graft_entry__.build())"
     lib = _native.load()
     assert lib.li_abi_version() == _native.ABI_VERSION
+
+
+def test_library_carries_the_digest_of_its_sources():
+    lib = _native.load()
+    assert lib.li_build_id().decode() == _build.source_hash()
+
+
+def test_a_library_built_from_other_sources_is_refused(monkeypatch):
+    """A stale build (its digest differs from the sources beside it) does not load."""
+    _native.load()
+    monkeypatch.setattr(_native, "_lib", None)
+    monkeypatch.setattr(_build, "source_hash", lambda: "0123456789abcdef")
+    with pytest.raises(RuntimeError, match="built from other sources"):
+        _native.load()
+    monkeypatch.undo()
+    assert _native.load().li_build_id().decode() == _build.source_hash()
 
 
 def test_every_declared_symbol_is_exported_and_bound():
