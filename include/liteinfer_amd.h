@@ -283,6 +283,23 @@ int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
                           size_t* workspace_bytes);
 
 /*
+ * The number of work-groups of a packed pass's prefill launch (`grid`
+ * work-groups) that fold its one-query rows first, as the launch computes it
+ * on the device: row_keys = the rows' total context, chunk_pairs = the
+ * chunks' visible causal (query, key) pairs, listed_blocks = the chunks'
+ * query blocks, split_waves = the waves whose partial slots the workspace
+ * holds (four row waves per work-group). Always within [0, min(grid,
+ * split_waves / 4)]; 0 when there are no rows. No counterpart in the
+ * reference, whose one-query rows run as prefill blocks; exported so that
+ * planners and tests see the same count the kernels use. Returns a negative
+ * code for a negative extent.
+ */
+int li_prefill_row_groups(unsigned long long row_keys,
+                          unsigned long long chunk_pairs, int listed_blocks,
+                          int grid, int split_waves, int num_kv_heads,
+                          int num_heads, int head_dim, int kv_fp8);
+
+/*
  * Packed / chunked prefill. Replaces paged_prefill
  * (liteinfer/models/paged_kernels.py:821-882) and _paged_prefill_kernel
  * (:416-459). Sequence i owns query rows [query_start_loc[i],

@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "li_paged_decode_ex",
     "li_paged_decode_noalloc",
     "li_paged_prefill_plan",
+    "li_prefill_row_groups",
     "li_paged_prefill",
     "li_paged_prefill_ex",
 )
@@ -97,6 +98,9 @@ _SIGNATURES = {
         _i32,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _p],
+    ),
+    "li_prefill_row_groups": (
+        _i32, [ctypes.c_ulonglong, ctypes.c_ulonglong, _i32, _i32, _i32, _i32, _i32, _i32, _i32],
     ),
     "li_paged_prefill_plan": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_sz)]),
     "li_paged_prefill": (

@@ -46,7 +46,8 @@ struct AttnArgs {
   int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
   int* queue;    // MFMA prefill: kPrefillQueues unit counters, the number of blocks listed in `work`, then
                  // (prefill_pp_rows) the number of work-groups that fold the one-query rows first
-  int row_groups_max;  // prefill_pp_rows: work-groups of its grid (0: the one-query rows are not in the launch)
+  int row_groups_max;  // prefill_pp_rows: most work-groups that may fold the rows, min(grid, d.num_parts /
+                       // kRowWaves) (0: the one-query rows are not in the launch)
   // fp8 (e4m3) pools: kp / vp hold K / k_scale and V / v_scale, one byte per
   // element (pool strides in bytes); the MFMA kernels only. Other pools hold
   // the query's dtype and ignore the scales.
@@ -56,6 +57,61 @@ struct AttnArgs {
 
 // Work queues of the persistent MFMA prefill grid (one per XCD).
 constexpr int kPrefillQueues = 8;
+
+// Decode waves per work-group of a prefill launch that folds the pass's
+// one-query rows first (prefill_pp_rows, prefill_mfma_rows).
+constexpr int kRowWaves = 4;
+
+// Flops of chunk work per byte of row K/V that put the rows' end at about
+// three quarters of the chunks' (prefill_row_groups): a CU of the ping-pong
+// kernel folds ~4.3 TFLOP/s of causal pairs (C3-like chunks, ~44% of the
+// bf16 peak over 256 CUs), and a work-group of four decode waves streams
+// ~36 GB/s beside the chunks' work-groups (both measured on MI355X: config
+// 3's step is flat at 307 us from 48 to 80 row work-groups and rises to
+// 340 / 407 us at 40 / 32), so the rows need B / 36e9 s of one CU for every
+// F / 4.3e12 s of chunks: 4.3e12 / (0.75 * 36e9) ~ 160.
+constexpr double kRowFlopsPerByte = 160.0;
+
+// Most work-groups of a prefill launch of `grid` work-groups that may fold
+// the one-query rows: each takes kRowWaves waves of a balanced split whose
+// workspace holds partial slots for `split_waves` waves.
+__host__ __device__ inline int prefill_row_cap(long long grid, int split_waves) {
+  const long long by_slots = split_waves > 0 ? split_waves / kRowWaves : 0;
+  const long long cap = grid < by_slots ? grid : by_slots;
+  return cap > 0 ? (int)cap : 0;
+}
+
+// How many work-groups of a prefill launch fold the one-query rows first:
+// the one rule the device (prefill_order) and the host-side planner and
+// tests use. row_keys: the rows' keys (sum of their contexts); chunk_pairs:
+// the chunks' visible causal (query, key) pairs; listed_blocks: the chunks'
+// query blocks; cap: the most row work-groups the launch can hold, which is
+// min(grid, partial slots of the workspace / kRowWaves), set on the host.
+// The rows' K/V bytes against the chunks' flops, scaled by
+// kRowFlopsPerByte, rounded to a multiple of the queue count (every XCD
+// gives the rows the same CUs), at least one per queue, and leaving each
+// chunk unit a work-group up to half the cap; never above `cap`, never
+// negative, 0 when there are no rows.
+__host__ __device__ inline int prefill_row_groups(unsigned long long row_keys, unsigned long long chunk_pairs,
+                                                  int listed_blocks, int cap, int num_kv_heads, int num_heads,
+                                                  int head_dim, int kv_fp8) {
+  if (cap <= 0 || row_keys == 0) return 0;
+  if (chunk_pairs == 0) return cap;
+  const double bytes = (double)row_keys * 2.0 * num_kv_heads * head_dim * (kv_fp8 ? 1.0 : 2.0);
+  const double flops = (double)chunk_pairs * 4.0 * num_heads * head_dim;
+  double want = cap * kRowFlopsPerByte * bytes / flops;
+  if (!(want < (double)cap)) want = (double)cap;  // also a NaN; keeps the conversion in range
+  const long long units = (long long)(listed_blocks > 0 ? listed_blocks : 0) * num_kv_heads;
+  long long keep = (units + kPrefillQueues - 1) / kPrefillQueues;
+  if (keep > cap / 2 / kPrefillQueues) keep = cap / 2 / kPrefillQueues;
+  keep *= kPrefillQueues;
+  if (keep < kPrefillQueues) keep = kPrefillQueues;
+  long long groups = (long long)(want / kPrefillQueues + 0.5) * kPrefillQueues;
+  const long long limit = (cap - keep) / kPrefillQueues * kPrefillQueues;
+  if (groups > limit) groups = limit;
+  if (groups < kPrefillQueues) groups = kPrefillQueues;
+  return (int)(groups < cap ? groups : cap);
+}
 
 // KV heads one wave of the head-grouped balanced decode folds together
 // (when num_kv_heads is a multiple of it).

@@ -383,6 +383,16 @@ extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads,
   return LI_OK;
 }
 
+extern "C" int li_prefill_row_groups(unsigned long long row_keys, unsigned long long chunk_pairs, int listed_blocks,
+                                     int grid, int split_waves, int num_kv_heads, int num_heads, int head_dim,
+                                     int kv_fp8) {
+  clear_error();
+  if (grid < 0 || split_waves < 0 || listed_blocks < 0 || num_kv_heads <= 0 || num_heads <= 0 || head_dim <= 0)
+    return fail(LI_EINVAL, "li_prefill_row_groups: negative or empty extent");
+  return prefill_row_groups(row_keys, chunk_pairs, listed_blocks, prefill_row_cap(grid, split_waves), num_kv_heads,
+                            num_heads, head_dim, kv_fp8);
+}
+
 int paged_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* key_pool,
                        const void* value_pool, int64_t pool_stride_slot, int64_t pool_stride_head,
                        const int64_t* slot_table, int64_t slot_table_stride, int max_context,

@@ -141,12 +141,13 @@ __device__ __forceinline__ void convert_stage(uint32_t raw, uint32_t dst, int ti
 // work-group's. (Three waves with three ring stages each, two tiles in
 // flight per wave, measured no faster: config 3 flat at 310-315 us from 48
 // row work-groups.)
-constexpr int kRowWaves = 4;
 
 template <typename T, int D, bool F8, typename Shared>
 __device__ __forceinline__ void fold_rows_first(const AttnArgs& a, const AttnArgs& d, Shared& lds) {
-  // prefill_order's count, held to what exists: every planned row wave is a
-  // wave of the grid and has partial slots in the workspace (d.num_parts).
+  // prefill_order's count (prefill_row_groups, at most a.row_groups_max,
+  // which the host holds to the grid and to the workspace's partial slots),
+  // held to both again here: every row wave is then a wave of the grid and
+  // has partial slots in the workspace (d.num_parts).
   const int row_groups = min(min(__builtin_amdgcn_readfirstlane(a.queue[kPrefillQueues + 1]), (int)gridDim.x),
                              d.num_parts / kRowWaves);
   const int wg = (int)blockIdx.x;
@@ -606,15 +607,6 @@ struct PpLds {
   int rows[3];  // the unit's first token + q0, its query count, first head
 };
 
-// Flops of chunk work per byte of row K/V that put the rows' end at about
-// three quarters of the chunks' (prefill_order's split): a CU of the
-// ping-pong kernel folds ~4.3 TFLOP/s of causal pairs (C3-like chunks,
-// ~44% of the bf16 peak over 256 CUs), and a work-group of four decode waves
-// streams ~36 GB/s beside the chunks' work-groups (both measured on MI355X:
-// config 3's step is flat at 307 us from 48 to 80 row work-groups and
-// rises to 340 / 407 us at 40 / 32), so the rows need B / 36e9 s of one CU
-// for every F / 4.3e12 s of chunks: 4.3e12 / (0.75 * 36e9) ~ 160.
-constexpr double kRowFlopsPerByte = 160.0;
 
 // LDS of a ping-pong work-group; prefill_pp_rows's row waves use it first.
 template <int D>
@@ -1211,24 +1203,9 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
       atomicAdd(&chunk_pairs, (unsigned long long)pairs);
     }
     __syncthreads();
-    if (tid == 0) {
-      const int g = a.row_groups_max;
-      int groups = 0;
-      if (row_keys > 0 && chunk_pairs == 0) {
-        groups = g;
-      } else if (row_keys > 0) {
-        const double bytes = (double)row_keys * 2.0 * a.num_kv_heads * a.head_dim * (a.kv_fp8 ? 1.0 : 2.0);
-        const double flops = (double)chunk_pairs * 4.0 * a.num_heads * a.head_dim;
-        const double want = g * kRowFlopsPerByte * bytes / flops;
-        // At most what leaves a work-group for each chunk unit, up to half
-        // the grid: the chunks' units all start at once when they are few.
-        const int units = max_tiles * a.num_kv_heads;
-        const int keep = min((units + kPrefillQueues - 1) / kPrefillQueues, g / 2 / kPrefillQueues) * kPrefillQueues;
-        groups = (int)(want / kPrefillQueues + 0.5) * kPrefillQueues;
-        groups = max(kPrefillQueues, min(groups, g - max(keep, kPrefillQueues)));
-      }
-      a.queue[kPrefillQueues + 1] = groups;
-    }
+    if (tid == 0)
+      a.queue[kPrefillQueues + 1] = prefill_row_groups(row_keys, chunk_pairs, max_tiles, a.row_groups_max,
+                                                       a.num_kv_heads, a.num_heads, a.head_dim, a.kv_fp8);
   }
 }
 
@@ -1269,7 +1246,12 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
   // there can be units (the rows' work-groups aside).
   int64_t grid = (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues;
   if (!rows) grid = std::min<int64_t>(grid, (units + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues);
-  a.row_groups_max = rows ? (int)grid : 0;
+  // The rows' waves must fit the workspace's partial slots as well as the
+  // grid: the one cap both prefill_order's rule and the kernel's clamp use.
+  a.row_groups_max = rows ? prefill_row_cap(grid, rows->num_parts) : 0;
+  if (rows && a.row_groups_max < 1)
+    return fail(LI_EINVAL, "prefill with rows: a split of %d waves holds no work-group of %d row waves",
+                rows->num_parts, kRowWaves);
   hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
   if (int rc = check_launch("prefill_order")) return rc;
   const dim3 block(64 * W);

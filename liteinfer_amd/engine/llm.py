@@ -70,24 +70,32 @@ class LLM:
         steps = decode_steps = 0
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        while self.scheduler.has_unfinished():
-            out = self.scheduler.schedule()
-            counts = [out.num_scheduled_tokens[s.request_id] for s in out.seqs]
-            logits = self.runner.execute(out.seqs, counts)
-            steps += 1
-            decode_steps += all(c == 1 for c in counts)
-            sample = [i for i, s in enumerate(out.seqs) if s.num_computed_tokens == len(s)]
-            if sample:
-                rows = torch.tensor(sample, device=logits.device)
-                tokens = logits.index_select(0, rows).argmax(dim=-1).tolist()
-                self.cache.pool.check_slot_writes()
-                for i, tok in zip(sample, tokens):
-                    seq = out.seqs[i]
-                    seq.output_token_ids.append(int(tok))
-                    if len(seq.output_token_ids) >= seq.max_tokens:
-                        seq.status = SequenceStatus.FINISHED_LENGTH
-            for seq in self.scheduler.remove_finished():
+        try:
+            while self.scheduler.has_unfinished():
+                out = self.scheduler.schedule()
+                counts = [out.num_scheduled_tokens[s.request_id] for s in out.seqs]
+                logits = self.runner.execute(out.seqs, counts)
+                steps += 1
+                decode_steps += all(c == 1 for c in counts)
+                sample = [i for i, s in enumerate(out.seqs) if s.num_computed_tokens == len(s)]
+                if sample:
+                    rows = torch.tensor(sample, device=logits.device)
+                    tokens = logits.index_select(0, rows).argmax(dim=-1).tolist()
+                    self.cache.pool.check_slot_writes()
+                    for i, tok in zip(sample, tokens):
+                        seq = out.seqs[i]
+                        seq.output_token_ids.append(int(tok))
+                        if len(seq.output_token_ids) >= seq.max_tokens:
+                            seq.status = SequenceStatus.FINISHED_LENGTH
+                for seq in self.scheduler.remove_finished():
+                    self.runner.release(seq)
+        except BaseException:
+            # A failed step (a slot write that missed the pool, a launch
+            # error) leaves no sequence holding cache blocks: the LLM stays
+            # usable for the next generate.
+            for seq in self.scheduler.abort_all():
                 self.runner.release(seq)
+            raise
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         self.cache.pool.check_slot_writes()

@@ -130,5 +130,11 @@ class Scheduler:
         self.running = kept
         return done
 
+    def abort_all(self) -> list[Sequence]:
+        """Drop every waiting and seated sequence (a failed step); returns them so their blocks can be freed."""
+        dropped = [*self.running, *self.waiting]
+        self.running, self.waiting = [], deque()
+        return dropped
+
     def has_unfinished(self) -> bool:
         return len(self.waiting) + len(self.running) > 0

@@ -87,3 +87,14 @@ def test_a_sequence_with_nothing_to_compute_is_an_error():
     s.num_computed_tokens = len(s)
     with pytest.raises(RuntimeError, match="no uncomputed token"):
         sched.schedule()
+
+
+def test_abort_all_returns_every_waiting_and_seated_sequence():
+    s = Scheduler(max_num_seqs=2, token_budget=1000)
+    seqs = [_seq(f"r{i}", 3) for i in range(5)]
+    for q in seqs:
+        s.add(q)
+    s.schedule()
+    dropped = s.abort_all()
+    assert sorted(q.request_id for q in dropped) == [q.request_id for q in seqs]
+    assert not s.has_unfinished() and s.schedule().seqs == []

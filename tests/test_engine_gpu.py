@@ -75,3 +75,31 @@ def test_fp8_cache_engine_logits_track_the_dense_forward(use_graphs):
         # e4m3 keeps 3 mantissa bits to bf16's 7: its rounding of the cached
         # K/V is up to 16x coarser than the dense bf16 forward's.
         print(check_tracks_dense(model, prompt, out, sampled_logits(steps, f"req-{i}"), slack=16.0))
+
+
+def test_a_failed_step_frees_the_batch_blocks_and_the_llm_runs_again():
+    """A step that raises (here: the slot-write check) leaves no sequence
+    holding cache blocks; the next generate runs on the whole pool."""
+    model = RandomLlama(TINY, dtype=torch.bfloat16, seed=4, std=0.05)
+    config = EngineConfig(max_num_seqs=4, max_model_len=256, max_num_batched_tokens=64, num_gpu_blocks=64)
+    llm = LLM(model, config)
+    pool = llm.cache.pool
+    free0 = pool.num_free_blocks
+    check = pool.check_slot_writes
+    calls = []
+
+    def failing():
+        calls.append(1)
+        if len(calls) == 2:
+            raise IndexError("1 K/V slot writes named a slot outside the pool")
+        check()
+
+    pool.check_slot_writes = failing
+    prompts = _prompts(6, 5, 70, TINY.vocab_size, seed=5)
+    with pytest.raises(IndexError):
+        llm.generate(prompts, max_tokens=4)
+    assert pool.num_free_blocks == free0
+    pool.check_slot_writes = check
+    outputs, _ = llm.generate(prompts, max_tokens=4)
+    assert [len(o) for o in outputs] == [4] * 6
+    assert pool.num_free_blocks == free0

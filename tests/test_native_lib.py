@@ -172,3 +172,59 @@ def test_scatter_rejects_null_pointers_before_launching():
                                _native.LI_BF16, None, None)
     assert status == _native.LI_EINVAL
     assert "null pointer" in _native.last_error()
+
+
+def _row_groups(row_keys, chunk_pairs, listed_blocks, grid=256, split_waves=1024, kv_heads=8, heads=32, dim=128,
+                fp8=0):
+    return _native.load().li_prefill_row_groups(row_keys, chunk_pairs, listed_blocks, grid, split_waves, kv_heads,
+                                                heads, dim, fp8)
+
+
+def test_prefill_row_groups_on_extreme_passes():
+    """The count of row work-groups a packed pass's prefill launch uses (the
+    rule prefill_order runs on the device), on the edges of its inputs: it
+    never exceeds the grid or the workspace's partial slots (four row waves
+    per work-group), whatever the passes' sizes."""
+    # no rows: none
+    assert _row_groups(0, 10**9, 100) == 0
+    # rows only: every work-group the launch can hold
+    assert _row_groups(5000, 0, 0) == 256
+    assert _row_groups(5000, 0, 0, grid=256, split_waves=512) == 128
+    # a workspace of exactly grid * 4 partial slots: the whole grid
+    assert _row_groups(5000, 0, 0, grid=264, split_waves=264 * 4) == 264
+    # a grid that is not a multiple of the four waves' slots (a CU count that
+    # is not a multiple of 8: grid 264, 1040 waves): held to the slots
+    assert _row_groups(5000, 0, 0, grid=264, split_waves=1040) == 260
+    assert _row_groups(10**7, 1, 1, grid=264, split_waves=1040) <= 260
+    # a grid smaller than the queue count: never above the grid
+    for grid in range(0, 9):
+        for keys, pairs, blocks in ((1, 1, 1), (10**6, 10**3, 1), (10, 10**12, 400), (10**6, 0, 0)):
+            got = _row_groups(keys, pairs, blocks, grid=grid, split_waves=4 * grid)
+            assert 0 <= got <= grid, (grid, keys, pairs, blocks, got)
+    # one tiny chunk against huge rows: the ratio overflows no integer
+    assert _row_groups(2**40, 1, 1) == 256 - 8
+    # one huge chunk against one short row: the floor of one per queue
+    assert _row_groups(1, 10**15, 1) == 8
+    # a workspace smaller than one work-group's waves: no row work-group
+    assert _row_groups(100, 100, 1, split_waves=3) == 0
+
+
+def test_prefill_row_groups_properties_on_a_grid_of_passes():
+    rng = __import__("random").Random(0)
+    for _ in range(3000):
+        grid = rng.choice([1, 7, 8, 64, 248, 256, 264, 304])
+        slots = rng.choice([0, 4, 4 * grid, 4 * grid - 4, 1024, 4 * grid + 40])
+        keys = rng.choice([0, 1, rng.randrange(1, 10**7), 2**50])
+        pairs = rng.choice([0, 1, rng.randrange(1, 10**12), 2**62])
+        blocks = rng.randrange(0, 5000)
+        fp8 = rng.randrange(2)
+        got = _row_groups(keys, pairs, blocks, grid=grid, split_waves=slots, fp8=fp8)
+        cap = min(grid, slots // 4)
+        assert 0 <= got <= cap
+        if keys == 0 or cap == 0:
+            assert got == 0
+        elif pairs == 0:
+            assert got == cap
+        elif got < cap:
+            assert got % 8 == 0 and got >= 8
+    assert _native.load().li_prefill_row_groups(1, 1, -1, 8, 32, 8, 32, 128, 0) == _native.LI_EINVAL
