@@ -239,6 +239,43 @@ int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q_stride_hea
                        size_t workspace_bytes, int dtype, int kv_dtype,
                        float k_scale, float v_scale, int flags, void* stream);
 
+/*
+ * One decode step of a layer: writes each sequence's newest K / V rows into
+ * the pool, then attends as li_paged_decode_ex does. Replaces the decode
+ * pair KVCache.scatter (liteinfer/cache/kv_cache.py:236-253, with the slots
+ * of newest_slots at position context_lens[i] - 1, block_pool.py:151-170)
+ * followed by paged_decode (liteinfer/models/paged_kernels.py:696-818).
+ *   new_key, new_value [batch, num_kv_heads, head_dim], strides
+ *                      (new_stride_seq, new_stride_head, 1), the query's
+ *                      dtype; written bit-exact (an fp8 pool: quantised as
+ *                      li_kv_scatter_fp8 does) to slot
+ *                      slot_table[i, context_lens[i] - 1], which must be
+ *                      part of no other sequence's context in this call;
+ *                      rows with an empty context write nothing. Both NULL:
+ *                      no write (a plain decode).
+ *   num_slots, bad_slots  the pool's slot count; a newest slot outside it is
+ *                      not written and is counted into *bad_slots (nullable).
+ * On the balanced head-grouped MFMA kernel over a 16-bit pool the write
+ * happens inside the decode launch (the wave folding a sequence's last key
+ * folds the new rows from registers and stores them); elsewhere a write
+ * launch runs first, with the same result. Everything else as
+ * li_paged_decode_ex; `workspace` as li_paged_decode_plan reports.
+ */
+int li_paged_decode_write(const void* q, int64_t q_stride_seq,
+                          int64_t q_stride_head, const void* key_pool,
+                          const void* value_pool, int64_t pool_stride_slot,
+                          int64_t pool_stride_head, const int64_t* slot_table,
+                          int64_t slot_table_stride, int max_context,
+                          const int32_t* context_lens, const void* new_key,
+                          const void* new_value, int64_t new_stride_seq,
+                          int64_t new_stride_head, int64_t num_slots,
+                          int32_t* bad_slots, void* out, int64_t out_stride_seq,
+                          int64_t out_stride_head, int batch, int num_heads,
+                          int num_kv_heads, int head_dim, float scale,
+                          int num_splits, int block_kv, void* workspace,
+                          size_t workspace_bytes, int dtype, int kv_dtype,
+                          float k_scale, float v_scale, int flags, void* stream);
+
 /* Bytes of device scratch li_paged_decode_noalloc holds per GPU. */
 #define LI_DECODE_NOALLOC_SCRATCH_BYTES (32u << 20)
 

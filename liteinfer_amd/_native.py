@@ -46,6 +46,7 @@ EXPORTED_SYMBOLS = (
     "li_paged_decode_plan",
     "li_paged_decode",
     "li_paged_decode_ex",
+    "li_paged_decode_write",
     "li_paged_decode_noalloc",
     "li_paged_prefill_plan",
     "li_prefill_row_groups",
@@ -94,6 +95,11 @@ _SIGNATURES = {
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
          _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _f32, _f32, _i32, _p],
     ),
+    "li_paged_decode_write": (
+        _i32,
+        [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
+         _i32, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz, _i32, _i32, _f32, _f32, _i32, _p],
+    ),
     "li_paged_decode_noalloc": (
         _i32,
         [_p, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _i32, _p, _p, _i64, _i64,
@@ -115,7 +121,7 @@ _SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

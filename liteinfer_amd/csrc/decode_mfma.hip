@@ -183,6 +183,28 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
       const char* vbase = static_cast<const char*>(a.vp) + h0 * head_bytes;
       const int64_t* srow = a.st + (int64_t)seq * a.st_s;
       const int kb = key0, ke = key0 + take;
+      // The sequence's newest K / V rows (a.new_k), when this wave folds its
+      // last key: lane (hd, kv, c) holds 16-byte chunk c of head h0 + hd's K
+      // (kv 0) or V (kv 1) row, in registers from here on. The pool's rows of
+      // that slot are read by no other wave of the launch (other groups read
+      // other heads' bytes), so this wave folds the new rows from registers
+      // and stores them after its last fold of the segment.
+      constexpr int kCh = D / 8;
+      const int nw_head = lane / (2 * kCh), nw_kv = (lane / kCh) & 1, nw_c = lane % kCh;
+      bool write_new = false;
+      u32x4_t new_row = {0u, 0u, 0u, 0u};
+      int64_t new_slot = 0;
+      if constexpr (!F8) {
+        write_new = a.new_k != nullptr && ke == ctx;
+        if (write_new) {
+          new_slot = srow[ctx - 1];
+          if (nw_head < HG) {
+            const T* src = static_cast<const T*>(nw_kv ? a.new_v : a.new_k) + (int64_t)seq * a.n_s0 +
+                           (int64_t)(h0 + nw_head) * a.n_s1 + 8 * nw_c;
+            new_row = *reinterpret_cast<const u32x4_t*>(src);
+          }
+        }
+      }
       for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
         const int c1 = min(c0 + kSlotChunk, ke);
         const int ntiles = (c1 - c0 + 31) / 32;
@@ -206,10 +228,38 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
             issue_tile<D, F8>(lds.stage[(h + 1) & 1], kbase + nh * head_bytes, vbase + nh * head_bytes, lds.sl,
                               row_bytes, min(32 * nt, kSlotChunk), lane);
             li_wait_vm<kInFlight>();
+            if constexpr (!F8) {
+              const int tk = c0 + 32 * ti;  // the tile's first key
+              if (write_new && tk + 32 >= ctx) {
+                // The tile holding key ctx - 1: its row, and the rows past it
+                // (their staged slot repeats that key's; masked, but they
+                // must hold finite values), take the new K / V, not what the
+                // pool held.
+                if (nw_head == h) {
+                  const uint32_t base = lds_addr(lds.stage[h & 1]) + (nw_kv ? 32 * L::kRowBytes : 0);
+                  for (int r = ctx - 1 - tk; r < 32; ++r) {
+                    const uint32_t at = base + (nw_kv ? L::voffset(r, nw_c) : L::offset(r, nw_c));
+                    *(__attribute__((address_space(3))) u32x4_t*)(uintptr_t)at = new_row;
+                  }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+              }
+            }
             fold_tile<T, D, F8>(lds_addr(lds.stage[h & 1]), c0 + 32 * ti, c1, q[h], sc * q[h].scale, off, st[h]);
           }
         }
         li_wait_vm<0>();
+      }
+      if (write_new) {
+        if (new_slot >= 0 && new_slot < a.num_slots) {
+          if (nw_head < HG) {
+            char* dst = static_cast<char*>(const_cast<void*>(nw_kv ? a.vp : a.kp)) + new_slot * row_bytes +
+                        (int64_t)(h0 + nw_head) * head_bytes + 16 * nw_c;
+            *reinterpret_cast<u32x4_t*>(dst) = new_row;
+          }
+        } else if (lane == 0 && grp == 0 && a.bad) {
+          atomicAdd(a.bad, 1);
+        }
       }
       const bool whole = key0 == 0 && take == ctx;
       const int slot = first_segment ? 0 : 1;

@@ -53,6 +53,15 @@ struct AttnArgs {
   // the query's dtype and ignore the scales.
   int kv_fp8;
   float k_scale, v_scale;
+  // Head-grouped decode over a 16-bit pool: each sequence's newest K / V
+  // rows, [batch, num_kv_heads, head_dim] with element strides (n_s0, n_s1,
+  // 1), written to slot st[seq, ctx - 1] by the wave that folds that key
+  // (which folds them from registers, not from the pool); nullptr: none.
+  const void* new_k;
+  const void* new_v;
+  int64_t n_s0, n_s1;
+  int64_t num_slots;  // the pool's slots: a newest row whose slot is outside is not stored
+  int* bad;           // nullable: counts sequences whose newest slot is outside the pool
 };
 
 // Work queues of the persistent MFMA prefill grid (one per XCD).

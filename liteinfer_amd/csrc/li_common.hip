@@ -50,7 +50,7 @@ int device_cu_count() {
 
 extern "C" const char* li_last_error_string(void) { return li::g_last_error.c_str(); }
 
-extern "C" int li_abi_version(void) { return 6; }
+extern "C" int li_abi_version(void) { return 7; }
 
 // Digest of the sources and flags this library was built from, passed in by
 // the build script; the Python loader refuses a library whose digest differs

@@ -94,6 +94,18 @@ size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int nu
          align256((size_t)batch * num_kv_heads * 16);
 }
 
+size_t newest_slot_bytes(int batch) { return align256((size_t)std::max(batch, 0) * sizeof(int64_t)); }
+
+// slots[i] = slot_table[i, ctx[i] - 1] (-1 for an empty context): where
+// li_paged_decode_write's newest rows go when a separate write stores them.
+__global__ __launch_bounds__(256) void newest_slots_kernel(const int64_t* table, int64_t table_stride,
+                                                           const int32_t* ctx, int batch, int64_t* slots) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= batch) return;
+  const int c = ctx[i];
+  slots[i] = c > 0 ? table[(int64_t)i * table_stride + c - 1] : -1;
+}
+
 // Points a balanced launch's partial buffers and piece table into `workspace`.
 void set_balanced(AttnArgs& d, int waves, void* workspace) {
   d.num_parts = waves;
@@ -117,6 +129,16 @@ int check_common(int dtype, int num_heads, int num_kv_heads, int head_dim, const
     return fail(LI_EUNSUPPORTED, "%s: head_dim %d is outside 1..%d", who, head_dim, kGenericMaxHeadDim);
   return LI_OK;
 }
+
+// li_paged_decode_write's newest K / V rows: [batch, num_kv_heads, head_dim]
+// with element strides (s0, s1, 1), for slot slot_table[i, ctx[i] - 1].
+struct NewestRows {
+  const void* k;  // nullptr: no rows to write
+  const void* v;
+  int64_t s0, s1;
+  int64_t num_slots;
+  int32_t* bad;
+};
 
 }  // namespace
 }  // namespace li
@@ -170,6 +192,9 @@ extern "C" int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads, 
   // current device's CU count whatever num_cus says, as the launch sizes it.
   need = std::max(need, balanced_workspace(balanced_waves(device_cu_count()), num_heads / num_kv_heads, head_dim,
                                            batch, num_kv_heads));
+  // Then the newest rows' slots li_paged_decode_write stages when its kernel
+  // does not write them itself.
+  need += newest_slot_bytes(batch);
   if (workspace_bytes) *workspace_bytes = need;
   return LI_OK;
 }
@@ -192,7 +217,7 @@ int paged_decode_impl(const void* q, int64_t q_stride_seq, int64_t q_stride_head
                       const int32_t* context_lens, void* out, int64_t out_stride_seq, int64_t out_stride_head,
                       int batch, int num_heads, int num_kv_heads, int head_dim, float scale, int num_splits,
                       int block_kv, void* workspace, size_t workspace_bytes, int dtype, int kv_dtype, float k_scale,
-                      float v_scale, int flags, void* stream) {
+                      float v_scale, int flags, void* stream, const NewestRows* newest = nullptr) {
   clear_error();
   if (int rc = check_common(dtype, num_heads, num_kv_heads, head_dim, "li_paged_decode")) return rc;
   if (int rc = check_kv(dtype, kv_dtype, k_scale, v_scale, "li_paged_decode")) return rc;
@@ -251,7 +276,41 @@ int paged_decode_impl(const void* q, int64_t q_stride_seq, int64_t q_stride_head
     return fail(LI_EUNSUPPORTED,
                 "li_paged_decode: fp8 pools run on the MFMA kernel only (bf16 / fp16 queries, head_dim 128, "
                 "16-byte aligned rows)");
-  if (mfma && (num_splits == 0 || !(flags & LI_FLAG_EQUAL_SPLITS))) {
+  const bool balanced = mfma && (num_splits == 0 || !(flags & LI_FLAG_EQUAL_SPLITS));
+  const bool grouped = balanced && balanced_part_heads(num_kv_heads) == kDecodeHeadGroup;
+  if (newest && newest->k) {
+    // The head-grouped kernel over a 16-bit pool writes the newest rows
+    // itself (16-byte aligned rows); anywhere else a write of them runs
+    // first, into the slots the table names.
+    const int esize = dtype_size(dtype);
+    const bool fused = grouped && !a.kv_fp8 && aligned16(newest->k) && aligned16(newest->v) &&
+                       (newest->s0 * esize) % 16 == 0 && (newest->s1 * esize) % 16 == 0;
+    if (fused) {
+      a.new_k = newest->k;
+      a.new_v = newest->v;
+      a.n_s0 = newest->s0;
+      a.n_s1 = newest->s1;
+      a.num_slots = newest->num_slots;
+      a.bad = newest->bad;
+    } else {
+      int64_t* slots = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + need - newest_slot_bytes(batch));
+      hipLaunchKernelGGL(newest_slots_kernel, dim3((unsigned)cdiv(batch, 256)), dim3(256), 0, s, slot_table,
+                         slot_table_stride, context_lens, batch, slots);
+      if (int rc = check_launch("newest_slots")) return rc;
+      const int64_t strides[4] = {newest->s0, newest->s1, 0, 1};
+      int rc = a.kv_fp8 ? li_kv_scatter_fp8(newest->k, newest->v, strides, strides, batch, 1, slots,
+                                            const_cast<void*>(key_pool), const_cast<void*>(value_pool),
+                                            newest->num_slots, pool_stride_slot, pool_stride_head, num_kv_heads,
+                                            head_dim, dtype, k_scale, v_scale, newest->bad, stream)
+                        : li_kv_scatter(newest->k, newest->v, strides, strides, batch, 1, slots,
+                                        const_cast<void*>(key_pool), const_cast<void*>(value_pool), newest->num_slots,
+                                        pool_stride_slot, pool_stride_head, num_kv_heads, head_dim, dtype,
+                                        newest->bad, stream);
+      if (rc) return rc;
+      clear_error();
+    }
+  }
+  if (balanced) {
     // The MFMA kernel's schedule: the balanced split (it launches its own
     // combine). A split count the caller chose (the engine passes
     // choose_num_splits's) is a scheduling hint; LI_FLAG_EQUAL_SPLITS makes
@@ -294,6 +353,28 @@ extern "C" int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q
                            slot_table, slot_table_stride, max_context, context_lens, out, out_stride_seq,
                            out_stride_head, batch, num_heads, num_kv_heads, head_dim, scale, num_splits, block_kv,
                            workspace, workspace_bytes, dtype, kv_dtype, k_scale, v_scale, flags, stream);
+}
+
+extern "C" int li_paged_decode_write(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+                                     const void* key_pool, const void* value_pool, int64_t pool_stride_slot,
+                                     int64_t pool_stride_head, const int64_t* slot_table, int64_t slot_table_stride,
+                                     int max_context, const int32_t* context_lens, const void* new_key,
+                                     const void* new_value, int64_t new_stride_seq, int64_t new_stride_head,
+                                     int64_t num_slots, int32_t* bad_slots, void* out, int64_t out_stride_seq,
+                                     int64_t out_stride_head, int batch, int num_heads, int num_kv_heads,
+                                     int head_dim, float scale, int num_splits, int block_kv, void* workspace,
+                                     size_t workspace_bytes, int dtype, int kv_dtype, float k_scale, float v_scale,
+                                     int flags, void* stream) {
+  clear_error();
+  if (!new_key != !new_value) return fail(LI_EINVAL, "li_paged_decode_write: give both newest K and V rows, or neither");
+  if (num_slots < 0) return fail(LI_EINVAL, "li_paged_decode_write: negative pool size");
+  if (new_key && (new_stride_seq < 0 || new_stride_head < 0))
+    return fail(LI_EINVAL, "li_paged_decode_write: negative newest-row strides");
+  const NewestRows newest{new_key, new_value, new_stride_seq, new_stride_head, num_slots, bad_slots};
+  return paged_decode_impl(q, q_stride_seq, q_stride_head, key_pool, value_pool, pool_stride_slot, pool_stride_head,
+                           slot_table, slot_table_stride, max_context, context_lens, out, out_stride_seq,
+                           out_stride_head, batch, num_heads, num_kv_heads, head_dim, scale, num_splits, block_kv,
+                           workspace, workspace_bytes, dtype, kv_dtype, k_scale, v_scale, flags, stream, &newest);
 }
 
 // The no-allocation decode: the workspace li_paged_decode would take lives in

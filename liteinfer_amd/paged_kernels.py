@@ -294,6 +294,8 @@ def paged_decode(
     kernel: str = "auto",
     k_scale: float = 1.0,
     v_scale: float = 1.0,
+    new_key: torch.Tensor | None = None,
+    new_value: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attend one query per sequence over the KV each sequence's slots address.
 
@@ -322,6 +324,14 @@ def paged_decode(
             whose rows hold K / k_scale and V / v_scale (`kv_scatter`); the
             attention is over the dequantised rows. fp8 pools run on the MFMA
             kernel (bf16 / fp16 queries, head_dim 128). Ignored otherwise.
+        new_key, new_value: each sequence's newest K / V rows, ``[batch,
+            num_kv_heads, head_dim]`` in the query's dtype, written into the
+            pool at the slot of its last context position (the decode
+            step's ``KVCache.scatter`` at ``newest_slots``, kv_cache.py:236-253)
+            before the attention reads it: one launch where the head-grouped
+            kernel serves the shape, a write launch first elsewhere. That slot
+            must belong to no other sequence's context in the call (as every
+            slot a `KVCache` hands out does).
 
     Returns:
         ``[batch, num_heads, head_dim]``, same dtype as ``query``.
@@ -331,6 +341,17 @@ def paged_decode(
     batch, num_heads, head_dim = query.shape
     num_kv_heads = key_pool.shape[1]
     max_context = slot_table.shape[1]
+    if (new_key is None) != (new_value is None):
+        raise ValueError("give both new_key and new_value, or neither")
+    if new_key is not None:
+        want = (batch, num_kv_heads, head_dim)
+        for name, t in (("new_key", new_key), ("new_value", new_value)):
+            if tuple(t.shape) != want or t.dtype != query.dtype or t.device != query.device:
+                raise ValueError(f"{name} must be {list(want)} {query.dtype} on {query.device}, "
+                                 f"got {list(t.shape)} {t.dtype} on {t.device}")
+        new_key, new_value = _last_dim_contiguous(new_key), _last_dim_contiguous(new_value)
+        if new_key.stride() != new_value.stride():
+            new_key, new_value = new_key.contiguous(), new_value.contiguous()
 
     lib = _native.load()
     parts, plen, need = _native.ctypes.c_int(), _native.ctypes.c_int(), _native.ctypes.c_size_t()
@@ -343,11 +364,15 @@ def paged_decode(
 
     out = torch.empty_like(query)
     workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
-    status = lib.li_paged_decode_ex(
+    status = lib.li_paged_decode_write(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
-        slot_table.data_ptr(), slot_table.stride(0), max_context,
-        context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+        slot_table.data_ptr(), slot_table.stride(0), max_context, context_lens.data_ptr(),
+        new_key.data_ptr() if new_key is not None else None,
+        new_value.data_ptr() if new_value is not None else None,
+        new_key.stride(0) if new_key is not None else 0, new_key.stride(1) if new_key is not None else 0,
+        key_pool.shape[0], None,
+        out.data_ptr(), out.stride(0), out.stride(1),
         batch, num_heads, num_kv_heads, head_dim, float(scaling),
         num_splits or 0, block_kv,
         workspace.data_ptr() if workspace is not None else None, need.value,
