@@ -42,7 +42,8 @@ def run(seed: int = 0, config: EngineConfig | None = None, num_requests: int = N
     if llm.runner.graphs is not None:
         llm.runner.graphs.capture_all()
     reqs = prompts(seed, n=num_requests)
-    _, stats = llm.generate(reqs, max_tokens=output_tokens)
+    outputs, stats = llm.generate(reqs, max_tokens=output_tokens)
+    vocab = model.shape.vocab_size
     return {
         "output_tok_per_s": round(stats.output_tokens_per_s, 1),
         "total_tok_per_s": round((stats.output_tokens + stats.prompt_tokens) / stats.wall_s, 1),
@@ -58,6 +59,11 @@ def run(seed: int = 0, config: EngineConfig | None = None, num_requests: int = N
         "decode_graphs": config.use_graphs,
         "kv_cache": config.cache_quant or "bf16",
         "parameter_bytes": model.parameter_bytes(),
+        # properties of the timed run's output, checked after the clock stops
+        "every_request_full_length": all(len(o) == output_tokens for o in outputs),
+        "tokens_in_vocab": all(0 <= t < vocab for o in outputs for t in o),
+        "sampled_logits_finite": stats.logits_finite,
+        "distinct_tokens": len({t for o in outputs for t in o}),
     }
 
 

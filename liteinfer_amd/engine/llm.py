@@ -40,6 +40,8 @@ class GenerateStats:
     decode_steps: int
     prompt_tokens: int
     output_tokens: int
+    logits_finite: bool = True
+    """Every logit row the step sampled from was finite."""
 
     @property
     def output_tokens_per_s(self) -> float:
@@ -68,6 +70,9 @@ class LLM:
             seqs.append(seq)
             self.scheduler.add(seq)
         steps = decode_steps = 0
+        # Finiteness of every sampled logit row, kept on the device (one
+        # small reduction per step, read once at the end).
+        finite = torch.ones((), dtype=torch.bool, device=self.model.device)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         try:
@@ -80,7 +85,9 @@ class LLM:
                 sample = [i for i, s in enumerate(out.seqs) if s.num_computed_tokens == len(s)]
                 if sample:
                     rows = torch.tensor(sample, device=logits.device)
-                    tokens = logits.index_select(0, rows).argmax(dim=-1).tolist()
+                    picked = logits.index_select(0, rows)
+                    finite &= torch.isfinite(picked).all()
+                    tokens = picked.argmax(dim=-1).tolist()
                     self.cache.pool.check_slot_writes()
                     for i, tok in zip(sample, tokens):
                         seq = out.seqs[i]
@@ -100,5 +107,5 @@ class LLM:
         wall = time.perf_counter() - t0
         self.cache.pool.check_slot_writes()
         stats = GenerateStats(wall, steps, decode_steps, sum(len(p) for p in prompts),
-                              sum(len(s.output_token_ids) for s in seqs))
+                              sum(len(s.output_token_ids) for s in seqs), bool(finite))
         return [s.output_token_ids for s in seqs], stats
