@@ -192,8 +192,18 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def stream_handle(device: torch.device) -> int:
-    """The current torch stream of `device`, as the hipStream_t the library takes."""
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current torch stream of `device`, as the hipStream_t the library takes.
+
+    Read through torch's raw-stream accessor (the handle itself, no Stream
+    object built per call); torch.cuda.current_stream where that is absent.
+    """
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def i64_array(values) -> ctypes.Array:

@@ -43,7 +43,8 @@ struct AttnArgs {
   int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
   int part_heads;  // balanced decode: KV heads per partial slot (1; kDecodeHeadGroup when head-grouped)
   int seg_cost;    // head-grouped decode: work units charged per segment start, on top of its 32-key tiles
-  int* work;     // MFMA prefill: query blocks (sequence * num_qblocks + block), heaviest first; -1 past the end
+  int4* work;    // MFMA prefill: query blocks, heaviest first, each {sequence * num_qblocks + block, the
+                 // sequence's first query row, its query count, its context length}; x = -1 past the end
   int* queue;    // MFMA prefill: kPrefillQueues unit counters, the number of blocks listed in `work`, then
                  // (prefill_pp_rows) the number of work-groups that fold the one-query rows first
   int row_groups_max;  // prefill_pp_rows: most work-groups that may fold the rows, min(grid, d.num_parts /
@@ -68,8 +69,16 @@ struct AttnArgs {
 constexpr int kPrefillQueues = 8;
 
 // Decode waves per work-group of a prefill launch that folds the pass's
-// one-query rows first (prefill_pp_rows, prefill_mfma_rows).
-constexpr int kRowWaves = 4;
+// one-query rows first (prefill_pp_rows, prefill_mfma_rows), and the tile
+// stages each such wave keeps in LDS.
+#ifndef LI_ROW_WAVES
+#define LI_ROW_WAVES 4
+#endif
+#ifndef LI_ROW_STAGES
+#define LI_ROW_STAGES 2
+#endif
+constexpr int kRowWaves = LI_ROW_WAVES;
+constexpr int kRowStages = LI_ROW_STAGES;
 
 // Flops of chunk work per byte of row K/V that put the rows' end at about
 // three quarters of the chunks' (prefill_row_groups): a CU of the ping-pong
@@ -79,7 +88,10 @@ constexpr int kRowWaves = 4;
 // 3's step is flat at 307 us from 48 to 80 row work-groups and rises to
 // 340 / 407 us at 40 / 32), so the rows need B / 36e9 s of one CU for every
 // F / 4.3e12 s of chunks: 4.3e12 / (0.75 * 36e9) ~ 160.
-constexpr double kRowFlopsPerByte = 160.0;
+#ifndef LI_ROW_FLOPS_PER_BYTE
+#define LI_ROW_FLOPS_PER_BYTE 160.0
+#endif
+constexpr double kRowFlopsPerByte = LI_ROW_FLOPS_PER_BYTE;
 
 // Most work-groups of a prefill launch of `grid` work-groups that may fold
 // the one-query rows: each takes kRowWaves waves of a balanced split whose
@@ -106,6 +118,9 @@ __host__ __device__ inline int prefill_row_groups(unsigned long long row_keys, u
                                                   int head_dim, int kv_fp8) {
   if (cap <= 0 || row_keys == 0) return 0;
   if (chunk_pairs == 0) return cap;
+#ifdef LI_ROW_GROUPS_FORCE
+  return LI_ROW_GROUPS_FORCE < cap ? LI_ROW_GROUPS_FORCE : cap;
+#endif
   const double bytes = (double)row_keys * 2.0 * num_kv_heads * head_dim * (kv_fp8 ? 1.0 : 2.0);
   const double flops = (double)chunk_pairs * 4.0 * num_heads * head_dim;
   double want = cap * kRowFlopsPerByte * bytes / flops;

@@ -447,7 +447,7 @@ extern "C" int li_paged_decode_noalloc(const void* q, int64_t q_stride_seq, int6
 // for the one-query sequences, then the prefill work list and its queues.
 size_t prefill_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads, int max_context) {
   return balanced_workspace(waves, groups, head_dim, batch, num_kv_heads) +
-         align256(prefill_work_entries(batch, max_context) * sizeof(int)) + align256((kPrefillQueues + 2) * sizeof(int));
+         align256(prefill_work_entries(batch, max_context) * sizeof(int4)) + align256((kPrefillQueues + 2) * sizeof(int));
 }
 
 extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,
@@ -535,10 +535,10 @@ int paged_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
     const size_t need = prefill_workspace(waves, a.groups, head_dim, batch, num_kv_heads, max_context);
     if (!workspace || workspace_bytes < need)
       return fail(LI_EWORKSPACE, "li_paged_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
-    a.work = reinterpret_cast<int*>(static_cast<char*>(workspace) +
+    a.work = reinterpret_cast<int4*>(static_cast<char*>(workspace) +
                                     balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads));
     a.queue = reinterpret_cast<int*>(reinterpret_cast<char*>(a.work) +
-                                     align256(prefill_work_entries(batch, max_context) * sizeof(int)));
+                                     align256(prefill_work_entries(batch, max_context) * sizeof(int4)));
     if (flags & LI_FLAG_PREFILL_ONLY) return launch_prefill_mfma(a, dtype, s);
     AttnArgs d = a;
     d.block_q = 1;

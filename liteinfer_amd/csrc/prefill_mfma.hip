@@ -177,7 +177,7 @@ struct LockstepLds {
 template <int D, bool F8>
 union LockstepShared {
   LockstepLds<D, F8> ls;
-  DecodeLds<D, F8> rows[kRowWaves];
+  DecodeLds<D, F8, kRowStages> rows[kRowWaves];
 };
 
 // F8: the pool is fp8 (e4m3, head_dim 128); its stages land raw and are
@@ -223,13 +223,15 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
   __syncthreads();
   const int unit = s_unit;
   if (unit >= units) break;
-  const int item = a.work[unit / heads_per_queue];
+  // The block's descriptor: one 16-byte read.
+  const int4 entry = a.work[unit / heads_per_queue];
+  const int item = entry.x;
   const int seq = item / a.num_qblocks;
   const int qblock = item % a.num_qblocks;
   const int kvh = qi + nqueues * (unit % heads_per_queue);
 
-  const int first_tok = a.qsl[seq];
-  const int nq = a.qsl[seq + 1] - first_tok;
+  const int first_tok = entry.y;
+  const int nq = entry.z;
   const int bq = a.block_q;  // query tokens per block = 32 W / groups
   // Blocks are cut from the end of the chunk: block nblk - 1 ends at its
   // last query and only block 0 (the one with the fewest keys) is partial.
@@ -238,7 +240,7 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
   const int q1 = nq - (nblk - 1 - qblock) * bq;
   const int q0 = max(q1 - bq, 0);
   if (nq == 1 && a.single_query_elsewhere) continue;  // the decode kernel serves it
-  const int ctx = a.ctx[seq];
+  const int ctx = entry.w;
   const int pos0 = ctx - nq;   // position of the sequence's first query
   const int kend = pos0 + q1;  // keys this block reads: [0, kend)
   const int G = a.groups;
@@ -605,6 +607,7 @@ struct PpLds {
   __attribute__((aligned(1024))) char vst[kPpRing][kRegion];
   int unit;
   int rows[3];  // the unit's first token + q0, its query count, first head
+  int4 entry;   // the work-list entry of `unit`
 };
 
 
@@ -612,7 +615,7 @@ struct PpLds {
 template <int D>
 union PpShared {
   PpLds<D> pp;
-  DecodeLds<D, false> rows[kRowWaves];
+  DecodeLds<D, false, kRowStages> rows[kRowWaves];
 };
 
 // The ping-pong work of work-group blockIdx.x of the persistent grid (its
@@ -654,33 +657,102 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   // stores and the loads in flight never hold a barrier up.
   int& s_unit = lds.pp.unit;
   auto& s_rows = lds.pp.rows;
-  if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
+  int4& s_entry = lds.pp.entry;
+  const int bq = a.block_q;
+  const int G = a.groups;
+  // Work-list entry of unit u (x = -1 past the end of the list).
+  auto entry_of = [&](int u) -> int4 { return u < units ? a.work[u / heads_per_queue] : int4{-1, 0, 0, 0}; };
+  // A listed block always has queries of its own (prefill_order lists only
+  // those); anything else is skipped rather than folded.
+  auto block_ok = [&](const int4& e) -> bool {
+    if (e.x < 0 || e.z <= 0 || (e.z == 1 && a.single_query_elsewhere)) return false;
+    return e.x % a.num_qblocks < (e.z + bq - 1) / bq;
+  };
+  if (tid == 0) {
+    const int u = atomicAdd(&a.queue[qi], 1);
+    s_unit = u;
+    s_entry = entry_of(u);
+  }
   int next_unit = 0;  // tid 0: the unit claimed for after this one
+  // The unit's queries (the softmax scale times log2 e folded in, rounded
+  // to T once: scores come out of the matrix cores in log2 units) and its
+  // first slots (the whole ring, or the unit's keys if fewer). A unit after
+  // the work-group's first has its slots read during the previous unit's
+  // epilogue (`have`), so that round trip overlaps the output stores
+  // instead of preceding the unit's first loads; its queries are read as
+  // its first stages are issued (and land with them). Reading the queries
+  // in the epilogue too made them live across the loop's back edge and
+  // spilled 24 registers.
+  const float sc = a.scale * kLog2eMfma;
+  constexpr int kSlotsPer = kSlotRing / (64 * W);
+  int first_slots[kSlotsPer];
+  Frag qf[2][kSteps];
+  bool have = false;
+  auto fetch_inputs = [&](const int4& e, int u, bool slots, bool queries) __attribute__((always_inline)) {
+    const int seq_ = e.x / a.num_qblocks, qb_ = e.x % a.num_qblocks;
+    const int nblk_ = (e.z + bq - 1) / bq;
+    const int q1_ = e.z - (nblk_ - 1 - qb_) * bq;
+    const int q0_ = max(q1_ - bq, 0);
+    const int kend_ = e.w - e.z + q1_;
+    const int kvh_ = qi + nqueues * (u % heads_per_queue);
+    const int64_t* srow_ = a.st + (int64_t)seq_ * a.st_s;
+    if (slots) {
+#pragma unroll
+      for (int r = 0; r < kSlotsPer; ++r) first_slots[r] = (int)srow_[min(tid + r * 64 * W, kend_ - 1)];
+    }
+    if (!queries) return;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int row = 32 * w + 16 * nb + n;
+      const int ql = row / G;
+      const bool real_ = row < bq * G && q0_ + ql < q1_;
+      const T* qrow = static_cast<const T*>(a.q) + (int64_t)(e.y + q0_ + ql) * a.q_s0 +
+                      (int64_t)(kvh_ * G + row % G) * a.q_s1 + 8 * g;
+#pragma unroll
+      for (int j = 0; j < kSteps; ++j) {
+        Frag x = real_ ? *reinterpret_cast<const Frag*>(qrow + 32 * j) : Frag{};
+        u32x4_t pw;
+#pragma unroll
+        for (int u2 = 0; u2 < 4; ++u2) pw[u2] = li_pack2<T>((float)x[2 * u2] * sc, (float)x[2 * u2 + 1] * sc);
+        qf[nb][j] = __builtin_bit_cast(Frag, pw);
+      }
+    }
+  };
   for (;;) {
   lds_barrier();
   // Values read from memory are made wave-uniform explicitly, so every
   // branch on them below is a scalar branch (no exec-masked code paths).
   const int unit = __builtin_amdgcn_readfirstlane(s_unit);
   if (unit >= units) break;
-  const int item = __builtin_amdgcn_readfirstlane(a.work[unit / heads_per_queue]);
+  const int4 entry{__builtin_amdgcn_readfirstlane(s_entry.x), __builtin_amdgcn_readfirstlane(s_entry.y),
+                   __builtin_amdgcn_readfirstlane(s_entry.z), __builtin_amdgcn_readfirstlane(s_entry.w)};
+  if (!block_ok(entry)) {
+    // (Never for a list prefill_order wrote.) Take the next unit; the
+    // barrier at the top orders these writes before every wave's reads.
+    lds_barrier();
+    if (tid == 0) {
+      const int u = atomicAdd(&a.queue[qi], 1);
+      s_unit = u;
+      s_entry = entry_of(u);
+    }
+    have = false;
+    continue;
+  }
+  const int item = entry.x;
   const int seq = item / a.num_qblocks;
   const int qblock = item % a.num_qblocks;
   const int kvh = qi + nqueues * (unit % heads_per_queue);
 
-  const int first_tok = __builtin_amdgcn_readfirstlane(a.qsl[seq]);
-  const int nq = __builtin_amdgcn_readfirstlane(a.qsl[seq + 1]) - first_tok;
-  const int bq = a.block_q;
+  const int first_tok = entry.y;
+  const int nq = entry.z;
   // Blocks are cut from the end of the chunk: block nblk - 1 ends at its
   // last query and only block 0 (the one with the fewest keys) is partial.
   const int nblk = (nq + bq - 1) / bq;
-  if (qblock >= nblk) continue;
   const int q1 = nq - (nblk - 1 - qblock) * bq;
   const int q0 = max(q1 - bq, 0);
-  if (nq == 1 && a.single_query_elsewhere) continue;
-  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx[seq]);
+  const int ctx = entry.w;
   const int pos0 = ctx - nq;
   const int kend = pos0 + q1;
-  const int G = a.groups;
   const int ns = (kend + kStageKeys - 1) / kStageKeys;  // 64-key stages
   // The next unit is claimed a few stages before this one ends, so the
   // atomic's round trip is hidden, yet late enough that a work-group that
@@ -693,39 +765,15 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     s_rows[2] = kvh * G;
   }
 
-  // The unit's first slots (the whole ring, or the unit's keys if fewer)
-  // are read here, before the queries, and written to the ring in the
-  // prologue: both reads share one round trip.
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
-  constexpr int kSlotsPer = kSlotRing / (64 * W);
-  int first_slots[kSlotsPer];
-#pragma unroll
-  for (int r = 0; r < kSlotsPer; ++r) first_slots[r] = (int)srow[min(tid + r * 64 * W, kend - 1)];
-
-  const float sc = a.scale * kLog2eMfma;
+  fetch_inputs(entry, unit, !have, true);
   int pos[2];
-  bool real[2];
-  int tok[2], head[2];
-  Frag qf[2][kSteps];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int row = 32 * w + 16 * nb + n;
     const int ql = row / G;
-    real[nb] = row < bq * G && q0 + ql < q1;
-    pos[nb] = real[nb] ? pos0 + q0 + ql : kend;
-    tok[nb] = first_tok + q0 + ql;
-    head[nb] = kvh * G + row % G;
-    const T* qrow = static_cast<const T*>(a.q) + (int64_t)tok[nb] * a.q_s0 + (int64_t)head[nb] * a.q_s1 + 8 * g;
-#pragma unroll
-    for (int j = 0; j < kSteps; ++j) {
-      // The softmax scale (times log2 e) is folded into the query, rounded
-      // to T once: scores come out of the matrix cores in log2 units.
-      Frag x = real[nb] ? *reinterpret_cast<const Frag*>(qrow + 32 * j) : Frag{};
-      u32x4_t pw;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) pw[u] = li_pack2<T>((float)x[2 * u] * sc, (float)x[2 * u + 1] * sc);
-      qf[nb][j] = __builtin_bit_cast(Frag, pw);
-    }
+    const bool real = row < bq * G && q0 + ql < q1;
+    pos[nb] = real ? pos0 + q0 + ql : kend;
   }
   const int lim[2] = {min(pos[0], kend - 1), min(pos[1], kend - 1)};
   const int lim_lo = min(pos0 + q0, kend - 1);
@@ -1001,6 +1049,10 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   // The last period: P V of the last stage only (every load has landed).
   li_wait_vm<0>();
   lds_barrier();
+  // tid 0 reads the next unit's work-list entry (its id came back from the
+  // claim above) while the last P V runs.
+  int4 next_entry{-1, 0, 0, 0};
+  if (tid == 0) next_entry = entry_of(next_unit);
   if (!idle) {
     Frag vf[2][kBlk];
     read_v(lds_addr(vst[(ns - 1) % kPpRing]) - lds_addr(vst[0]), vf);
@@ -1008,7 +1060,20 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   }
   lds_barrier();
   if (!late) lds_barrier();  // the barrier waves 4-7 took first
-  if (tid == 0) s_unit = next_unit;
+  if (tid == 0) {
+    s_unit = next_unit;
+    s_entry = next_entry;
+  }
+  lds_barrier();
+  {
+    // The next unit's first slots, read now so that their round trip runs
+    // under this unit's output stores.
+    const int nu = __builtin_amdgcn_readfirstlane(s_unit);
+    const int4 ne{__builtin_amdgcn_readfirstlane(s_entry.x), __builtin_amdgcn_readfirstlane(s_entry.y),
+                  __builtin_amdgcn_readfirstlane(s_entry.z), __builtin_amdgcn_readfirstlane(s_entry.w)};
+    have = nu < units && block_ok(ne);
+    if (have) fetch_inputs(ne, nu, true, false);
+  }
 
   // The output rows, normalised. A lane holds 8-byte pieces of its row 32
   // bytes apart, so stored as they are every store instruction would write
@@ -1169,7 +1234,9 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   __syncthreads();
   auto place = [&](int sq, int nb, int t) {
     const int at = atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
-    for (int i = 0; i < nb; ++i) a.work[at + i] = sq * a.num_qblocks + (nb - 1 - i);
+    const int first = a.qsl[sq];
+    const int4 e{0, first, a.qsl[sq + 1] - first, a.ctx[sq]};
+    for (int i = 0; i < nb; ++i) a.work[at + i] = int4{sq * a.num_qblocks + (nb - 1 - i), e.y, e.z, e.w};
   };
   if (c_nb > 0) place(tid, c_nb, c_t);
   for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
@@ -1178,7 +1245,7 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
     if (nb > 0) place(sq, nb, t);
   }
   const int items = a.batch * a.num_qblocks;
-  for (int i = max_tiles + tid; i < items; i += 1024) a.work[i] = -1;
+  for (int i = max_tiles + tid; i < items; i += 1024) a.work[i] = int4{-1, 0, 0, 0};
   // The persistent grid's queues start empty for this launch.
   if (tid < kPrefillQueues) a.queue[tid] = 0;
   if (tid == 0) a.queue[kPrefillQueues] = max_tiles;
