@@ -90,16 +90,11 @@ __device__ __forceinline__ void issue_tile(char* stage, const char* __restrict__
   }
 }
 
-// LDS of one decode wave: the staged slots of a chunk and kStages tile
-// stages (two: the next tile's loads land while one is folded; one: a wave
-// loads, waits and folds in turn, for work-groups that run many such waves).
-template <int D, bool F8, int kStages = 2>
+// LDS of one decode wave: the staged slots of a chunk and two tile stages.
+template <int D, bool F8>
 struct DecodeLds {
-  // Keys whose slots are staged at a time (one-stage waves stage half as
-  // many, so eight of them fit beside nothing else in a CU's LDS).
-  static constexpr int kChunk = kStages == 1 ? kSlotChunk / 2 : kSlotChunk;
-  int sl[kChunk + 64];
-  char stage[kStages][KvTile<D, F8>::kTileBytes];
+  int sl[kSlotChunk + 64];
+  char stage[2][KvTile<D, F8>::kTileBytes];
 };
 
 // Online-softmax state of one wave: lane (n, g) holds head n's running max
@@ -299,10 +294,9 @@ __device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const 
 }
 
 // Folds keys [kb, ke) of sequence `seq`'s context for KV head `kvh` into `st`.
-template <typename T, int D, bool F8, int kStages>
-__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8, kStages>& lds,
-                                          const DecodeQuery<T, D, F8>& q, int seq, int kvh, int kb, int ke,
-                                          DecodeState& st) {
+template <typename T, int D, bool F8>
+__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& lds, const DecodeQuery<T, D, F8>& q,
+                                          int seq, int kvh, int kb, int ke, DecodeState& st) {
   using L = KvTile<D, F8>;
   const int lane = li_lane();
   const TileOffsets<D, F8> off;
@@ -313,37 +307,26 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8, kS
   const int64_t* srow = a.st + (int64_t)seq * a.st_s;
   // An fp8 pool stores K / k_scale: its scale multiplies the scores.
   const float sc = a.scale * (F8 ? a.k_scale * q.scale : 1.f) * kLog2eMfma;
-  constexpr int kChunk = DecodeLds<D, F8, kStages>::kChunk;
 
-  for (int c0 = kb; c0 < ke; c0 += kChunk) {
-    const int c1 = min(c0 + kChunk, ke);
+  for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
+    const int c1 = min(c0 + kSlotChunk, ke);
     const int ntiles = (c1 - c0 + 31) / 32;
     // Stage this chunk's slots (int32: a pool holds fewer than 2^31 slots),
     // plus a tile past its end. Entries past the chunk repeat its last slot,
     // so the loads of a partial or look-ahead tile read real rows; their
     // scores are masked.
     {
-      int vals[kChunk / 64 + 1];
+      int vals[kSlotChunk / 64 + 1];
 #pragma unroll
-      for (int k = 0; k < kChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
+      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
 #pragma unroll
-      for (int k = 0; k < kChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
+      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
     }
 
     auto fold = [&](uint32_t stage, int t0) __attribute__((always_inline)) {
       fold_tile<T, D, F8>(stage, t0, c1, q, sc, off, st);
     };
 
-    if constexpr (kStages == 1) {
-      // One stage: load a tile, wait for it, fold it (its LDS reads are done
-      // when the fold returns), then the next.
-      for (int ti = 0; ti < ntiles; ++ti) {
-        issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, 32 * ti, lane);
-        li_wait_vm<0>();
-        fold(lds_addr(lds.stage[0]), c0 + 32 * ti);
-      }
-      continue;
-    }
     // Two stages: while one tile is folded the next tile's loads land in the
     // other. Past the chunk the look-ahead re-reads a real tile (cache hits),
     // so the loads in flight are the same every step and no load sits under
@@ -351,11 +334,11 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8, kS
     constexpr int kInFlight = 2 * L::kInsts;
     issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, 0, lane);
     for (int ti = 0;;) {
-      issue_tile<D, F8>(lds.stage[1], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kChunk), lane);
+      issue_tile<D, F8>(lds.stage[1], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
       fold(lds_addr(lds.stage[0]), c0 + 32 * ti);
       if (++ti >= ntiles) break;
-      issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kChunk), lane);
+      issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kSlotChunk), lane);
       li_wait_vm<kInFlight>();
       fold(lds_addr(lds.stage[1]), c0 + 32 * ti);
       if (++ti >= ntiles) break;
@@ -480,9 +463,8 @@ __device__ __forceinline__ void balanced_share(const AttnArgs& a, int64_t waves,
 }
 
 // One wave's share of the balanced split: wave w of `waves` (its LDS `lds`).
-template <typename T, int D, bool F8, int kStages>
-__device__ __forceinline__ void decode_balanced_wave(const AttnArgs& a, int w, int64_t waves,
-                                                     DecodeLds<D, F8, kStages>& lds) {
+template <typename T, int D, bool F8>
+__device__ __forceinline__ void decode_balanced_wave(const AttnArgs& a, int w, int64_t waves, DecodeLds<D, F8>& lds) {
   const float vscale = F8 ? a.v_scale : 1.f;
   const int lane = li_lane();
   int64_t total, share;
@@ -544,7 +526,7 @@ __device__ __forceinline__ void decode_balanced_wave(const AttnArgs& a, int w, i
     load_query(a, row, kvh, q);
     DecodeState st;
     reset_state(st);
-    fold_keys<T, D, F8, kStages>(a, lds, q, seq, kvh, key0, key0 + take, st);
+    fold_keys<T, D, F8>(a, lds, q, seq, kvh, key0, key0 + take, st);
     if (key0 == 0 && take == ctx) {
       store_state<T, D>(st, static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)kvh * G * a.o_s1, a.o_s1,
                         nullptr, nullptr, 0, G, vscale);

@@ -69,16 +69,11 @@ struct AttnArgs {
 constexpr int kPrefillQueues = 8;
 
 // Decode waves per work-group of a prefill launch that folds the pass's
-// one-query rows first (prefill_pp_rows, prefill_mfma_rows), and the tile
-// stages each such wave keeps in LDS.
-#ifndef LI_ROW_WAVES
-#define LI_ROW_WAVES 4
-#endif
-#ifndef LI_ROW_STAGES
-#define LI_ROW_STAGES 2
-#endif
-constexpr int kRowWaves = LI_ROW_WAVES;
-constexpr int kRowStages = LI_ROW_STAGES;
+// one-query rows first (prefill_pp_rows, prefill_mfma_rows). (Eight waves
+// of one tile stage each measured the same row throughput per work-group,
+// ~36-40 GB/s: a CU gathers scattered 256-byte rows at up to ~50 GB/s
+// whether into LDS or registers, by a standalone probe.)
+constexpr int kRowWaves = 4;
 
 // Flops of chunk work per byte of row K/V that put the rows' end at about
 // three quarters of the chunks' (prefill_row_groups): a CU of the ping-pong
@@ -88,10 +83,7 @@ constexpr int kRowStages = LI_ROW_STAGES;
 // 3's step is flat at 307 us from 48 to 80 row work-groups and rises to
 // 340 / 407 us at 40 / 32), so the rows need B / 36e9 s of one CU for every
 // F / 4.3e12 s of chunks: 4.3e12 / (0.75 * 36e9) ~ 160.
-#ifndef LI_ROW_FLOPS_PER_BYTE
-#define LI_ROW_FLOPS_PER_BYTE 160.0
-#endif
-constexpr double kRowFlopsPerByte = LI_ROW_FLOPS_PER_BYTE;
+constexpr double kRowFlopsPerByte = 160.0;
 
 // Most work-groups of a prefill launch of `grid` work-groups that may fold
 // the one-query rows: each takes kRowWaves waves of a balanced split whose
@@ -118,9 +110,6 @@ __host__ __device__ inline int prefill_row_groups(unsigned long long row_keys, u
                                                   int head_dim, int kv_fp8) {
   if (cap <= 0 || row_keys == 0) return 0;
   if (chunk_pairs == 0) return cap;
-#ifdef LI_ROW_GROUPS_FORCE
-  return LI_ROW_GROUPS_FORCE < cap ? LI_ROW_GROUPS_FORCE : cap;
-#endif
   const double bytes = (double)row_keys * 2.0 * num_kv_heads * head_dim * (kv_fp8 ? 1.0 : 2.0);
   const double flops = (double)chunk_pairs * 4.0 * num_heads * head_dim;
   double want = cap * kRowFlopsPerByte * bytes / flops;

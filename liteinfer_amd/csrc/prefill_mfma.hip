@@ -177,7 +177,7 @@ struct LockstepLds {
 template <int D, bool F8>
 union LockstepShared {
   LockstepLds<D, F8> ls;
-  DecodeLds<D, F8, kRowStages> rows[kRowWaves];
+  DecodeLds<D, F8> rows[kRowWaves];
 };
 
 // F8: the pool is fp8 (e4m3, head_dim 128); its stages land raw and are
@@ -615,7 +615,7 @@ struct PpLds {
 template <int D>
 union PpShared {
   PpLds<D> pp;
-  DecodeLds<D, false, kRowStages> rows[kRowWaves];
+  DecodeLds<D, false> rows[kRowWaves];
 };
 
 // The ping-pong work of work-group blockIdx.x of the persistent grid (its
