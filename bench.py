@@ -486,6 +486,31 @@ def _only_prefill(workload: str, seed: int, steps: int, warmup: int) -> int:
     return 0
 
 
+def _copy_calibration() -> None:
+    """Three 1 GiB device-to-device copies: a kernel of known traffic for rocprofv3's counters."""
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def _only_step(seed: int, steps: int, warmup: int) -> int:
+    """Config 2's fused step alone (eager calls, then graph replays), for profiling."""
+    step = decode_step("c2", seed=seed)
+    geo = step.geometry
+    wall, step_ms = _time_step(step, steps, warmup)
+    d_bytes = decode_bytes(step.host_context_lens, geo)
+    w_bytes = 4 * step.batch * geo.num_kv_heads * geo.head_dim * 2
+    avg = statistics.mean(step_ms)
+    print(json.dumps({"workload": "c2_step", "avg_launch_us": round(avg * 1e3, 2),
+                      "ms_per_step_graph": round(wall / steps * 1e3, 5),
+                      "algorithmic_bytes_per_launch": d_bytes + w_bytes,
+                      "frac_hbm": round((d_bytes + w_bytes) / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -500,10 +525,16 @@ def main() -> int:
                              "size for rocprofv3 FETCH_SIZE / WRITE_SIZE calibration)")
     parser.add_argument("--only-prefill", choices=["c3", "c3_fp8", "c3_chunks", "long"],
                         help="time only this packed prefill pass (for profiling) and print its line")
+    parser.add_argument("--only-step", action="store_true",
+                        help="time only config 2's fused decode step (for profiling) and print its line")
     args = parser.parse_args()
 
     if args.only_prefill and args.gpus == 1:
         return _only_prefill(args.only_prefill, args.seed, args.steps, args.warmup)
+    if args.only_step and args.gpus == 1:
+        if args.copy_calibration:
+            _copy_calibration()
+        return _only_step(args.seed, args.steps, args.warmup)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build's paged path has no multi-GPU component "
               "(decode shards by sequence or KV head with no exchange inside attention); run with --gpus 1.",
@@ -515,12 +546,7 @@ def main() -> int:
     _native.load()
     torch.cuda.set_device(0)
     if args.copy_calibration:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        _copy_calibration()
 
     step = decode_step("c2", seed=args.seed)
     geo = step.geometry
