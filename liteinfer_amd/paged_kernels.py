@@ -280,6 +280,19 @@ def _decode_inputs(query, key_pool, value_pool, slot_table, context_lens, num_kv
     return device, query, slot_table, context_lens, kv_code
 
 
+@functools.lru_cache(maxsize=4096)
+def _decode_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, max_context: int,
+                            num_splits: int, device_index: int, block_kv: int) -> int:
+    """li_paged_decode_plan's workspace size for one shape: a function of these host integers only, so it
+    is asked once per shape (a decode step calls it once per layer with the same shape)."""
+    parts, plen, need = _native.ctypes.c_int(), _native.ctypes.c_int(), _native.ctypes.c_size_t()
+    status = _native.load().li_paged_decode_plan(
+        batch, num_heads, num_kv_heads, head_dim, max_context, num_splits, _compute_unit_count(device_index),
+        block_kv, _native.ctypes.byref(parts), _native.ctypes.byref(plen), _native.ctypes.byref(need))
+    _native.check(status, "paged_decode")
+    return need.value
+
+
 def paged_decode(
     query: torch.Tensor,
     key_pool: torch.Tensor,
@@ -354,16 +367,10 @@ def paged_decode(
             new_key, new_value = new_key.contiguous(), new_value.contiguous()
 
     lib = _native.load()
-    parts, plen, need = _native.ctypes.c_int(), _native.ctypes.c_int(), _native.ctypes.c_size_t()
-    status = lib.li_paged_decode_plan(
-        batch, num_heads, num_kv_heads, head_dim, max_context, num_splits or 0,
-        _compute_unit_count(device.index or 0), block_kv,
-        _native.ctypes.byref(parts), _native.ctypes.byref(plen), _native.ctypes.byref(need),
-    )
-    _native.check(status, "paged_decode")
-
+    need = _decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, max_context, num_splits or 0,
+                                   device.index or 0, block_kv)
     out = torch.empty_like(query)
-    workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
+    workspace = torch.empty(need, dtype=torch.uint8, device=device) if need else None
     status = lib.li_paged_decode_write(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
@@ -375,7 +382,7 @@ def paged_decode(
         out.data_ptr(), out.stride(0), out.stride(1),
         batch, num_heads, num_kv_heads, head_dim, float(scaling),
         num_splits or 0, block_kv,
-        workspace.data_ptr() if workspace is not None else None, need.value,
+        workspace.data_ptr() if workspace is not None else None, need,
         _native.dtype_code(query.dtype), kv_code, float(k_scale), float(v_scale),
         _flags(kernel), _native.stream_handle(device),
     )
@@ -424,6 +431,17 @@ def paged_decode_noalloc(
     )
     _native.check(status, "paged_decode_noalloc")
     return out
+
+
+@functools.lru_cache(maxsize=4096)
+def _prefill_workspace_bytes(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, max_context: int,
+                             device_index: int) -> int:
+    """li_paged_prefill_plan's workspace size for one shape (host integers only; asked once per shape)."""
+    need = _native.ctypes.c_size_t()
+    status = _native.load().li_paged_prefill_plan(batch, num_heads, num_kv_heads, head_dim, max_context,
+                                                  _compute_unit_count(device_index), _native.ctypes.byref(need))
+    _native.check(status, "paged_prefill")
+    return need.value
 
 
 def paged_prefill(
@@ -504,18 +522,13 @@ def paged_prefill(
     max_context = slot_table.shape[1]
 
     lib = _native.load()
-    need = _native.ctypes.c_size_t()
-    status = lib.li_paged_prefill_plan(
-        batch, num_heads, num_kv_heads, head_dim, max_context, _compute_unit_count(device.index or 0),
-        _native.ctypes.byref(need),
-    )
-    _native.check(status, "paged_prefill")
+    need = _prefill_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, max_context, device.index or 0)
     if out is None:
         out = torch.empty_like(query)
     elif (out.shape != query.shape or out.dtype != query.dtype or out.device != query.device
           or out.stride(-1) != 1):
         raise ValueError("out must match the query's shape, dtype and device, with a contiguous last axis")
-    workspace = torch.empty(need.value, dtype=torch.uint8, device=device) if need.value else None
+    workspace = torch.empty(need, dtype=torch.uint8, device=device) if need else None
     status = lib.li_paged_prefill_ex(
         query.data_ptr(), query.stride(0), query.stride(1),
         key_pool.data_ptr(), value_pool.data_ptr(), key_pool.stride(0), key_pool.stride(1),
@@ -523,7 +536,7 @@ def paged_prefill(
         context_lens.data_ptr(), query_start_loc.data_ptr(), batch, int(max_query_len),
         out.data_ptr(), out.stride(0), out.stride(1),
         num_heads, num_kv_heads, head_dim, float(scaling), block_q, block_kv,
-        workspace.data_ptr() if workspace is not None else None, need.value,
+        workspace.data_ptr() if workspace is not None else None, need,
         _native.dtype_code(query.dtype), kv_code, float(k_scale), float(v_scale),
         _flags(_prefill_kernel(kernel)) | (_native.LI_FLAG_PREFILL_ONLY if one_query_rows is False else 0),
         _native.stream_handle(device),
