@@ -1,8 +1,12 @@
-"""The generate loop (liteinfer/llm.py `LLM.generate` over the engine core), greedy
-and token-id only: each step schedules, runs one forward, samples the argmax
-for every sequence whose prompt is complete, and retires sequences that reached
-their `max_tokens` (stop strings and EOS do not apply: the end-to-end
-configuration fixes every output at its length).
+"""The generate loop (liteinfer/llm.py `LLM.generate` over the engine core), greedy:
+each step schedules, runs one forward, samples the argmax for every sequence
+whose prompt is complete, and retires sequences that reached their
+`max_tokens` (stop strings and EOS do not apply: the end-to-end configuration
+fixes every output at its length).
+
+`generate(prompts, sampling_params)` takes text and returns `RequestOutput`s
+through a local tokenizer, as the reference's `LLM.generate` does;
+`generate_ids` is the same loop on token ids, with the step statistics.
 """
 
 from __future__ import annotations
@@ -15,8 +19,10 @@ import torch
 from liteinfer_amd.cache.block_pool import BlockPool
 from liteinfer_amd.cache.kv_cache import KVCache
 from liteinfer_amd.engine.model import RandomLlama
+from liteinfer_amd.engine.outputs import RequestOutput, SamplingParams
 from liteinfer_amd.engine.runner import ModelRunner
 from liteinfer_amd.engine.scheduler import Scheduler, Sequence, SequenceStatus
+from liteinfer_amd.engine.tokenizer import Tokenizer
 
 
 @dataclass
@@ -49,10 +55,13 @@ class GenerateStats:
 
 
 class LLM:
-    def __init__(self, model: RandomLlama, config: EngineConfig = EngineConfig()) -> None:
+    def __init__(self, model: RandomLlama, config: EngineConfig = EngineConfig(),
+                 tokenizer: Tokenizer | None = None) -> None:
         s = model.shape
         self.config = config
         self.model = model
+        self.tokenizer = tokenizer
+        self.stats: GenerateStats | None = None  # the last generate call's step statistics
         pool = BlockPool(num_blocks=config.num_gpu_blocks, block_size=config.block_size, num_layers=s.num_layers,
                          num_kv_heads=s.num_kv_heads, head_dim=s.head_dim, dtype=model.dtype, device=model.device,
                          cache_quant=config.cache_quant, k_scale=config.k_scale, v_scale=config.v_scale)
@@ -60,8 +69,30 @@ class LLM:
         self.runner = ModelRunner(model, self.cache, config.max_num_seqs, config.max_model_len, config.use_graphs)
         self.scheduler = Scheduler(config.max_num_seqs, config.max_num_batched_tokens)
 
-    def generate(self, prompts: list[list[int]], max_tokens: int) -> tuple[list[list[int]], GenerateStats]:
-        """Greedy continuation of every prompt to exactly `max_tokens` tokens."""
+    def generate(self, prompts: str | list[str], sampling_params: SamplingParams | None = None) -> list[RequestOutput]:
+        """Completions of text prompts, in the order given (liteinfer/llm.py:49-55).
+
+        Greedy and fixed-length: `sampling_params` must ask for temperature 0
+        with no top-p / top-k / stop strings, and every output runs to
+        `max_tokens` (the tokenizer has no end-of-sequence token).
+        """
+        if self.tokenizer is None:
+            raise ValueError("this LLM has no tokenizer: pass one, or call generate_ids with token ids")
+        params = sampling_params or SamplingParams(temperature=0.0)
+        if not params.greedy or params.top_p != 1.0 or params.top_k != -1 or params.stop or params.stop_token_ids:
+            raise ValueError("this engine samples greedily: temperature 0, no top-p / top-k / stop conditions")
+        texts = [prompts] if isinstance(prompts, str) else list(prompts)
+        ids = [self.tokenizer.encode(t) for t in texts]
+        for i, p in enumerate(ids):
+            if not p:
+                raise ValueError(f"prompt {i} encodes to no tokens")
+        outputs, stats = self.generate_ids(ids, params.max_tokens)
+        self.stats = stats
+        return [RequestOutput(f"req-{i}", text, self.tokenizer.decode(out), out, "length")
+                for i, (text, out) in enumerate(zip(texts, outputs))]
+
+    def generate_ids(self, prompts: list[list[int]], max_tokens: int) -> tuple[list[list[int]], GenerateStats]:
+        """Greedy continuation of every token-id prompt to exactly `max_tokens` tokens."""
         seqs = []
         for i, p in enumerate(prompts):
             if len(p) + max_tokens > self.config.max_model_len:

@@ -45,7 +45,7 @@ def _generate(model, use_graphs):
     steps = record_logits(llm)
     prompts = e2e.prompts(seed=0, n=REQUESTS)
     assert sum(len(p) for p in prompts) <= 65536
-    outputs, stats = llm.generate(prompts, max_tokens=OUTPUT_TOKENS)
+    outputs, stats = llm.generate_ids(prompts, max_tokens=OUTPUT_TOKENS)
     del llm
     torch.cuda.empty_cache()
     return prompts, outputs, stats, steps

@@ -98,3 +98,33 @@ def test_abort_all_returns_every_waiting_and_seated_sequence():
     dropped = s.abort_all()
     assert sorted(q.request_id for q in dropped) == [q.request_id for q in seqs]
     assert not s.has_unfinished() and s.schedule().seqs == []
+
+
+def test_wordlevel_tokenizer_round_trips_token_ids(tmp_path):
+    from liteinfer_amd.engine.tokenizer import Tokenizer, make_wordlevel
+
+    make_wordlevel(1000, tmp_path)
+    tok = Tokenizer(tmp_path)
+    assert tok.vocab_size == 1000 and tok.eos_token_ids == ()
+    ids = [0, 999, 17, 17, 500]
+    text = " ".join(f"tok{i}" for i in ids)
+    assert tok.encode(text) == ids
+    assert tok.decode(ids) == text
+    assert tok.encode("  tok3\ttok4\n") == [3, 4]
+
+
+def test_tokenizer_reads_local_files_only(tmp_path):
+    from liteinfer_amd.engine.tokenizer import Tokenizer
+
+    with pytest.raises(FileNotFoundError):
+        Tokenizer(tmp_path / "missing")
+
+
+def test_sampling_params_checks_follow_the_reference():
+    from liteinfer_amd.engine.outputs import SamplingParams
+
+    assert SamplingParams(temperature=0.0).greedy
+    for bad in ({"temperature": -1}, {"top_p": 0.0}, {"top_k": 0}, {"max_tokens": 0}, {"min_tokens": -1},
+                {"max_tokens": 4, "min_tokens": 5}):
+        with pytest.raises(ValueError):
+            SamplingParams(**bad)

@@ -32,7 +32,7 @@ def test_greedy_outputs_match_a_dense_forward_fp32(use_graphs):
     config = EngineConfig(max_num_seqs=4, max_model_len=256, max_num_batched_tokens=48, num_gpu_blocks=128,
                           use_graphs=use_graphs)
     prompts = _prompts(6, 5, 70, TINY.vocab_size)  # more requests than slots, prompts longer than the budget
-    outputs, stats = LLM(model, config).generate(prompts, max_tokens=6)
+    outputs, stats = LLM(model, config).generate_ids(prompts, max_tokens=6)
     assert stats.output_tokens == 36 and stats.decode_steps > 0
     for prompt, out in zip(prompts, outputs):
         seq = list(prompt)
@@ -48,7 +48,7 @@ def test_bf16_engine_logits_track_the_dense_forward():
     llm = LLM(model, config)
     steps = record_logits(llm)
     prompts = _prompts(5, 40, 200, TINY.vocab_size, seed=3)
-    outputs, _ = llm.generate(prompts, max_tokens=3)
+    outputs, _ = llm.generate_ids(prompts, max_tokens=3)
     for i, (prompt, out) in enumerate(zip(prompts, outputs)):
         assert len(out) == 3
         print(check_tracks_dense(model, prompt, out, sampled_logits(steps, f"req-{i}")))
@@ -69,7 +69,7 @@ def test_fp8_cache_engine_logits_track_the_dense_forward(use_graphs):
     assert llm.cache.pool.cache_quant == "fp8"
     steps = record_logits(llm)
     prompts = _prompts(5, 40, 200, TINY128.vocab_size, seed=5)
-    outputs, stats = llm.generate(prompts, max_tokens=3)
+    outputs, stats = llm.generate_ids(prompts, max_tokens=3)
     assert stats.output_tokens == 15
     for i, (prompt, out) in enumerate(zip(prompts, outputs)):
         # e4m3 keeps 3 mantissa bits to bf16's 7: its rounding of the cached
@@ -97,9 +97,32 @@ def test_a_failed_step_frees_the_batch_blocks_and_the_llm_runs_again():
     pool.check_slot_writes = failing
     prompts = _prompts(6, 5, 70, TINY.vocab_size, seed=5)
     with pytest.raises(IndexError):
-        llm.generate(prompts, max_tokens=4)
+        llm.generate_ids(prompts, max_tokens=4)
     assert pool.num_free_blocks == free0
     pool.check_slot_writes = check
-    outputs, _ = llm.generate(prompts, max_tokens=4)
+    outputs, _ = llm.generate_ids(prompts, max_tokens=4)
     assert [len(o) for o in outputs] == [4] * 6
     assert pool.num_free_blocks == free0
+
+
+def test_text_prompts_round_trip_through_the_tokenizer(tmp_path):
+    """LLM.generate(prompts, SamplingParams) as the reference's (liteinfer/llm.py:49-55): text in,
+    RequestOutputs out, the same tokens as the token-id loop, the text their decoding."""
+    from liteinfer_amd.engine.outputs import SamplingParams
+    from liteinfer_amd.engine.tokenizer import Tokenizer, make_wordlevel
+
+    make_wordlevel(TINY.vocab_size, tmp_path)
+    tok = Tokenizer(tmp_path)
+    model = RandomLlama(TINY, dtype=torch.bfloat16, seed=6, std=0.05)
+    config = EngineConfig(max_num_seqs=4, max_model_len=256, max_num_batched_tokens=64, num_gpu_blocks=128)
+    ids = _prompts(5, 3, 40, TINY.vocab_size, seed=7)
+    texts = [" ".join(f"tok{t}" for t in p) for p in ids]
+    llm = LLM(model, config, tokenizer=tok)
+    results = llm.generate(texts, SamplingParams(temperature=0.0, max_tokens=5, ignore_eos=True))
+    want, _ = LLM(model, config).generate_ids(ids, max_tokens=5)
+    assert [r.token_ids for r in results] == want
+    assert [r.prompt for r in results] == texts
+    assert all(r.text == tok.decode(r.token_ids) and r.finish_reason == "length" for r in results)
+    assert llm.stats is not None and llm.stats.output_tokens == 25
+    with pytest.raises(ValueError, match="greedily"):
+        llm.generate(texts[:1], SamplingParams(temperature=0.7))

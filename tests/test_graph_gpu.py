@@ -180,7 +180,7 @@ def test_plain_capture_after_an_engine_capture():
     config = EngineConfig(max_num_seqs=4, max_model_len=128, max_num_batched_tokens=64, num_gpu_blocks=64,
                           use_graphs=True)
     llm = LLM(model, config)
-    outputs, stats = llm.generate([[1, 2, 3, 4], [5, 6, 7]], max_tokens=4)
+    outputs, stats = llm.generate_ids([[1, 2, 3, 4], [5, 6, 7]], max_tokens=4)
     assert [len(o) for o in outputs] == [4, 4] and stats.decode_steps > 0
     assert llm.runner.graphs.captured_widths, "the engine captured no decode graph"
 
