@@ -96,14 +96,22 @@ size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int nu
 
 size_t newest_slot_bytes(int batch) { return align256((size_t)std::max(batch, 0) * sizeof(int64_t)); }
 
-// slots[i] = slot_table[i, ctx[i] - 1] (-1 for an empty context): where
-// li_paged_decode_write's newest rows go when a separate write stores them.
+// slots[i] = slot_table[i, ctx[i] - 1]: where li_paged_decode_write's newest
+// rows go when a separate write stores them; -1 (skipped by the write) for
+// an empty context, and for a slot outside the pool, which is counted into
+// *bad as the fused kernel counts it.
 __global__ __launch_bounds__(256) void newest_slots_kernel(const int64_t* table, int64_t table_stride,
-                                                           const int32_t* ctx, int batch, int64_t* slots) {
+                                                           const int32_t* ctx, int batch, int64_t num_slots,
+                                                           int32_t* bad, int64_t* slots) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= batch) return;
   const int c = ctx[i];
-  slots[i] = c > 0 ? table[(int64_t)i * table_stride + c - 1] : -1;
+  int64_t slot = c > 0 ? table[(int64_t)i * table_stride + c - 1] : -1;
+  if (c > 0 && (slot < 0 || slot >= num_slots)) {
+    if (bad) atomicAdd(bad, 1);
+    slot = -1;
+  }
+  slots[i] = slot;
 }
 
 // Points a balanced launch's partial buffers and piece table into `workspace`.
@@ -295,17 +303,17 @@ int paged_decode_impl(const void* q, int64_t q_stride_seq, int64_t q_stride_head
     } else {
       int64_t* slots = reinterpret_cast<int64_t*>(static_cast<char*>(workspace) + need - newest_slot_bytes(batch));
       hipLaunchKernelGGL(newest_slots_kernel, dim3((unsigned)cdiv(batch, 256)), dim3(256), 0, s, slot_table,
-                         slot_table_stride, context_lens, batch, slots);
+                         slot_table_stride, context_lens, batch, newest->num_slots, newest->bad, slots);
       if (int rc = check_launch("newest_slots")) return rc;
       const int64_t strides[4] = {newest->s0, newest->s1, 0, 1};
       int rc = a.kv_fp8 ? li_kv_scatter_fp8(newest->k, newest->v, strides, strides, batch, 1, slots,
                                             const_cast<void*>(key_pool), const_cast<void*>(value_pool),
                                             newest->num_slots, pool_stride_slot, pool_stride_head, num_kv_heads,
-                                            head_dim, dtype, k_scale, v_scale, newest->bad, stream)
+                                            head_dim, dtype, k_scale, v_scale, nullptr, stream)
                         : li_kv_scatter(newest->k, newest->v, strides, strides, batch, 1, slots,
                                         const_cast<void*>(key_pool), const_cast<void*>(value_pool), newest->num_slots,
                                         pool_stride_slot, pool_stride_head, num_kv_heads, head_dim, dtype,
-                                        newest->bad, stream);
+                                        nullptr, stream);
       if (rc) return rc;
       clear_error();
     }
