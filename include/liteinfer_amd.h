@@ -382,6 +382,28 @@ int li_paged_prefill_ex(const void* q, int64_t q_stride_tok, int64_t q_stride_he
                         size_t workspace_bytes, int dtype, int kv_dtype,
                         float k_scale, float v_scale, int flags, void* stream);
 
+/*
+ * The minimal engine's per-layer elementwise work (the model around the
+ * paged path; no counterpart in the reference's paged path, which leaves it
+ * to torch ops). Rows of `hidden` (a multiple of 8, at most 8192) bf16 / fp16
+ * elements, 16-byte aligned, last axis contiguous; strides in elements.
+ *
+ * li_add_rms_norm: when `delta` is given, h <- h + delta (rounded to the
+ * dtype, in place); then out <- weight * dtype(h * rsqrt(mean(h^2) + eps)),
+ * the product rounded to the dtype: the residual add and RMSNorm of
+ * liteinfer/models/llama.py:34-48 (fp32 statistics) in one launch.
+ * li_silu_mul: out[r, :] <- silu(gate) * up with gate = gate_up[r, :ffn],
+ * up = gate_up[r, ffn:2 ffn] (the SiLU gate of llama.py:101-116), each of the
+ * two products rounded to the dtype as torch rounds them.
+ */
+int li_add_rms_norm(void* h, const void* delta, const void* weight, void* out,
+                    int64_t rows, int hidden, int64_t h_stride,
+                    int64_t delta_stride, int64_t out_stride, float eps,
+                    int dtype, void* stream);
+int li_silu_mul(const void* gate_up, void* out, int64_t rows, int ffn,
+                int64_t gate_up_stride, int64_t out_stride, int dtype,
+                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,12 +52,16 @@ EXPORTED_SYMBOLS = (
     "li_prefill_row_groups",
     "li_paged_prefill",
     "li_paged_prefill_ex",
+    "li_add_rms_norm",
+    "li_silu_mul",
 )
 
 _i64, _i32, _p, _f32, _sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
 _i64p = ctypes.POINTER(ctypes.c_int64)
 
 _SIGNATURES = {
+    "li_add_rms_norm": (_i32, [_p, _p, _p, _p, _i64, _i32, _i64, _i64, _i64, _f32, _i32, _p]),
+    "li_silu_mul": (_i32, [_p, _p, _i64, _i32, _i64, _i64, _i32, _p]),
     "li_last_error_string": (ctypes.c_char_p, []),
     "li_abi_version": (_i32, []),
     "li_build_id": (ctypes.c_char_p, []),

@@ -421,9 +421,12 @@ __device__ __forceinline__ int decode_row(const AttnArgs& a, int seq) {
   return (a.qsl[seq + 1] - f == 1) ? f : -1;
 }
 
-// Keys of sequence `seq` the decode kernel folds, per KV head.
+// Keys of sequence `seq` the decode kernel folds, per KV head. The context
+// length is read beside the query rows (not after them, as the branch would
+// order it): in a packed pass the two reads then share one round trip.
 __device__ __forceinline__ int decode_keys(const AttnArgs& a, int seq) {
-  return decode_row(a, seq) < 0 ? 0 : max(a.ctx[seq], 0);
+  const int ctx = a.ctx[seq];
+  return decode_row(a, seq) < 0 ? 0 : max(ctx, 0);
 }
 
 // ---------------------------------------------------------------------------

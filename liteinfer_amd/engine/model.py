@@ -77,6 +77,15 @@ class RandomLlama:
         self.final_norm = torch.ones(shape.hidden_size, device=self.device, dtype=dtype)
         self.lm_head = (torch.randn(shape.vocab_size, shape.hidden_size, generator=gen, device=self.device,
                                     dtype=torch.float32) * std).to(dtype)
+        # 16-bit models on the GPU run the residual adds, RMSNorms and SiLU
+        # gate as fused HIP kernels (engine/ops.py); fp32 models (the exact
+        # references of the engine tests) keep the torch ops.
+        self._fused_ops = None
+        if (self.device.type == "cuda" and dtype in (torch.bfloat16, torch.float16)
+                and shape.hidden_size % 8 == 0 and shape.hidden_size <= 8192 and shape.intermediate_size % 8 == 0):
+            from liteinfer_amd.engine import ops
+
+            self._fused_ops = ops
         d = shape.head_dim
         # The "default" rope type: no frequency scaling (llama.py:62-67).
         self.inv_freq = 1.0 / (shape.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32, device=self.device) / d))
@@ -116,8 +125,13 @@ class RandomLlama:
         h = F.embedding(input_ids, self.embed)
         cos, sin = self._rotary(positions)
         nq, nkv = s.num_heads, s.num_kv_heads
+        fused = self._fused_ops
+        delta = None  # the MLP output not yet added to the residual stream
         for idx, layer in enumerate(self.layers):
-            x = self._rms_norm(h, layer.attn_norm)
+            if fused:
+                x = fused.add_rms_norm(h, layer.attn_norm, s.rms_norm_eps, delta)
+            else:
+                x = self._rms_norm(h, layer.attn_norm)
             qkv = F.linear(x, layer.w_qkv).view(batch, tokens, nq + 2 * nkv, s.head_dim)
             q = qkv[:, :, :nq].transpose(1, 2)
             k = qkv[:, :, nq:nq + nkv].transpose(1, 2)
@@ -125,10 +139,17 @@ class RandomLlama:
             q, kv = payload.update_rotated(q, k, v, cos, sin, idx)
             attn = paged_attention(q, kv, self.scaling, s.groups)
             attn = attn.transpose(1, 2).reshape(batch, tokens, nq * s.head_dim)
-            h = h + F.linear(attn, layer.w_o)
-            x = self._rms_norm(h, layer.mlp_norm)
-            gate, up = F.linear(x, layer.w_gate_up).chunk(2, dim=-1)
-            h = h + F.linear(F.silu(gate) * up, layer.w_down)
-        h = self._rms_norm(h, self.final_norm)
+            if fused:
+                x = fused.add_rms_norm(h, layer.mlp_norm, s.rms_norm_eps, F.linear(attn, layer.w_o))
+                delta = F.linear(fused.silu_mul(F.linear(x, layer.w_gate_up)), layer.w_down)
+            else:
+                h = h + F.linear(attn, layer.w_o)
+                x = self._rms_norm(h, layer.mlp_norm)
+                gate, up = F.linear(x, layer.w_gate_up).chunk(2, dim=-1)
+                h = h + F.linear(F.silu(gate) * up, layer.w_down)
+        if fused:
+            h = fused.add_rms_norm(h, self.final_norm, s.rms_norm_eps, delta)
+        else:
+            h = self._rms_norm(h, self.final_norm)
         rows = h[0, logits_positions] if logits_positions is not None else h[:, -1]
         return F.linear(rows, self.lm_head)
