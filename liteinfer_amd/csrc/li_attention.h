@@ -44,7 +44,8 @@ struct AttnArgs {
   int part_heads;  // balanced decode: KV heads per partial slot (1; kDecodeHeadGroup when head-grouped)
   int seg_cost;    // head-grouped decode: work units charged per segment start, on top of its 32-key tiles
   int4* work;    // MFMA prefill: query blocks, heaviest first, each {sequence * num_qblocks + block, the
-                 // sequence's first query row, its query count, its context length}; x = -1 past the end
+                 // sequence's first query row, its query count, its context length}; only the first
+                 // queue[kPrefillQueues] entries are written
   int* queue;    // MFMA prefill: kPrefillQueues unit counters, the number of blocks listed in `work`, then
                  // (prefill_pp_rows) the number of work-groups that fold the one-query rows first
   int row_groups_max;  // prefill_pp_rows: most work-groups that may fold the rows, min(grid, d.num_parts /

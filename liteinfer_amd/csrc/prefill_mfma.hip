@@ -660,7 +660,8 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   int4& s_entry = lds.pp.entry;
   const int bq = a.block_q;
   const int G = a.groups;
-  // Work-list entry of unit u (x = -1 past the end of the list).
+  // Work-list entry of unit u ({-1, ...} for a unit past the listed ones,
+  // without reading the list there).
   auto entry_of = [&](int u) -> int4 { return u < units ? a.work[u / heads_per_queue] : int4{-1, 0, 0, 0}; };
   // A listed block always has queries of its own (prefill_order lists only
   // those); anything else is skipped rather than folded.
@@ -1149,8 +1150,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // Work list of the prefill grid: every non-empty query block
 // (sequence * num_qblocks + block), a sequence's blocks side by side, last
 // (heaviest) block first, the sequences ordered by the 32-key tiles of their
-// heaviest block, most first (a counting sort on tiles >> shift), then -1 up
-// to batch * num_qblocks. Work-groups take units in this order as earlier
+// heaviest block, most first (a counting sort on tiles >> shift), each with
+// the sequence's rows and context; their count goes to queue[kPrefillQueues]
+// and nothing past it is read. Work-groups take units in this order as earlier
 // ones retire, so the long blocks start at once and the short ones fill in
 // behind them (longest-processing-time-first, by sequence), and the
 // work-groups running at one time on an XCD fold blocks of one sequence:
@@ -1165,20 +1167,26 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   __shared__ int max_tiles;
   __shared__ unsigned long long row_keys, chunk_pairs;  // prefill_pp_rows's balance
   const int tid = threadIdx.x;
-  // Blocks of sequence `seq` the prefill folds, and the tiles of its
-  // heaviest (last) block.
-  auto blocks_of = [&](int seq, int* tiles) {
-    const int first = a.qsl[seq];
-    const int nq = a.qsl[seq + 1] - first;
+  // A sequence's first query row, query count and context length: three
+  // independent reads, one round trip.
+  auto info_of = [&](int seq) -> int4 {
+    const int first = a.qsl[seq], next = a.qsl[seq + 1], ctx = a.ctx[seq];
+    return int4{first, next - first, ctx, 0};
+  };
+  // Blocks of a sequence the prefill folds, and the tiles of its heaviest
+  // (last) block.
+  auto blocks_of = [&](const int4& e, int* tiles) {
+    const int nq = e.y;
     *tiles = 0;
     if (nq <= 0 || (nq == 1 && a.single_query_elsewhere)) return 0;
-    *tiles = (a.ctx[seq] + 31) / 32;
+    *tiles = (e.z + 31) / 32;
     return min((nq + a.block_q - 1) / a.block_q, a.num_qblocks);
   };
   // A thread's first sequence (the only one while batch <= 1024) is read
-  // once and kept for all three passes; further ones are read again.
+  // once and kept for every pass; further ones are read again.
+  const int4 c_e = tid < a.batch ? info_of(tid) : int4{0, 0, 0, 0};
   int c_t = 0;
-  const int c_nb = tid < a.batch ? blocks_of(tid, &c_t) : 0;
+  const int c_nb = tid < a.batch ? blocks_of(c_e, &c_t) : 0;
   if (tid < kOrderBins) hist[tid] = 0;
   if (tid == 0) {
     max_tiles = 0;
@@ -1189,7 +1197,7 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   int local = c_t;
   for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
     int t;
-    blocks_of(sq, &t);
+    blocks_of(info_of(sq), &t);
     local = max(local, t);
   }
 #pragma unroll
@@ -1203,7 +1211,7 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   if (c_nb > 0) atomicAdd(&hist[kOrderBins - 1 - (c_t >> shift)], c_nb);
   for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
     int t;
-    const int nb = blocks_of(sq, &t);
+    const int nb = blocks_of(info_of(sq), &t);
     if (nb > 0) atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
   }
   __syncthreads();
@@ -1232,20 +1240,19 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
     }
   }
   __syncthreads();
-  auto place = [&](int sq, int nb, int t) {
+  auto place = [&](int sq, const int4& e, int nb, int t) {
     const int at = atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
-    const int first = a.qsl[sq];
-    const int4 e{0, first, a.qsl[sq + 1] - first, a.ctx[sq]};
-    for (int i = 0; i < nb; ++i) a.work[at + i] = int4{sq * a.num_qblocks + (nb - 1 - i), e.y, e.z, e.w};
+    for (int i = 0; i < nb; ++i) a.work[at + i] = int4{sq * a.num_qblocks + (nb - 1 - i), e.x, e.y, e.z};
   };
-  if (c_nb > 0) place(tid, c_nb, c_t);
+  if (c_nb > 0) place(tid, c_e, c_nb, c_t);
   for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
     int t;
-    const int nb = blocks_of(sq, &t);
-    if (nb > 0) place(sq, nb, t);
+    const int4 e = info_of(sq);
+    const int nb = blocks_of(e, &t);
+    if (nb > 0) place(sq, e, nb, t);
   }
-  const int items = a.batch * a.num_qblocks;
-  for (int i = max_tiles + tid; i < items; i += 1024) a.work[i] = int4{-1, 0, 0, 0};
+  // Entries past the listed blocks are never read: the prefill kernels take
+  // units below the listed count only.
   // The persistent grid's queues start empty for this launch.
   if (tid < kPrefillQueues) a.queue[tid] = 0;
   if (tid == 0) a.queue[kPrefillQueues] = max_tiles;
@@ -1258,8 +1265,9 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
     // XCD gives the rows the same number of CUs.
     int64_t keys = 0, pairs = 0;
     for (int sq = tid; sq < a.batch; sq += 1024) {
-      const int nq = a.qsl[sq + 1] - a.qsl[sq];
-      const int c = max(a.ctx[sq], 0);
+      const int4 e = sq == tid ? c_e : info_of(sq);
+      const int nq = e.y;
+      const int c = max(e.z, 0);
       if (nq == 1) keys += c;
       else if (nq > 1) pairs += (int64_t)nq * max(c - nq, 0) + (int64_t)nq * (nq + 1) / 2;
     }
