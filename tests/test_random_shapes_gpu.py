@@ -125,3 +125,45 @@ def test_prefill_random_long_chunks(case):
         out = paged_prefill(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.query_start_loc,
                             max(q), b.scaling, b.groups, one_query_rows=one_query_rows)
         assert_within(out, b.oracle(), 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_decode_step_with_newest_rows_random_shapes(case):
+    """paged_decode(new_key=, new_value=) against the scatter-then-decode pair on the same pools: the
+    pools and the attention bit for bit, whatever the shape (each sequence's slots its own, as a cache
+    hands them out)."""
+    from liteinfer_amd.cache.kv_cache import scatter_into
+
+    rng = np.random.default_rng(7500 + case)
+    num_heads, num_kv_heads = _heads(rng)
+    head_dim = int(rng.choice([64, 128]))
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    batch = int(rng.integers(1, 120))
+    ctx = _contexts(rng, batch, int(rng.choice([600, 3000])))
+    num_slots = sum(ctx) + max(ctx) + 64
+    g = torch.Generator().manual_seed(7500 + case)
+    kp = torch.randn(num_slots, num_kv_heads, head_dim, generator=g).to(dtype).cuda()
+    vp = torch.randn(num_slots, num_kv_heads, head_dim, generator=g).to(dtype).cuda()
+    q = torch.randn(batch, num_heads, head_dim, generator=g).to(dtype).cuda()
+    nk = torch.randn(batch, num_kv_heads, head_dim, generator=g).to(dtype).cuda()
+    nv = torch.randn(batch, num_kv_heads, head_dim, generator=g).to(dtype).cuda()
+    perm = torch.randperm(num_slots, generator=g)
+    width = max(ctx)
+    table = torch.empty(batch, width, dtype=torch.int64)
+    at = 0
+    for i, c in enumerate(ctx):
+        table[i, :c] = perm[at:at + c]
+        table[i, c:] = perm[-(width - c):] if width > c else table[i, c:]
+        at += c
+    table = table.cuda()
+    lens = torch.tensor(ctx, dtype=torch.int32, device="cuda")
+    groups, scale = num_heads // num_kv_heads, head_dim ** -0.5
+    kp1, vp1 = kp.clone(), vp.clone()
+    fused = paged_decode(q, kp1, vp1, table, lens, scale, groups, new_key=nk, new_value=nv)
+    newest = table.gather(1, (lens.long() - 1)[:, None]).view(1, -1)
+    scatter_into(kp, vp, newest, nk.unsqueeze(2), nv.unsqueeze(2))
+    paired = paged_decode(q, kp, vp, table, lens, scale, groups)
+    torch.cuda.synchronize()
+    assert torch.equal(kp1.view(torch.int16), kp.view(torch.int16))
+    assert torch.equal(vp1.view(torch.int16), vp.view(torch.int16))
+    assert torch.equal(fused.view(torch.int16), paired.view(torch.int16))
