@@ -76,20 +76,28 @@ __global__ __launch_bounds__(64) void decode_balanced(AttnArgs a) {
 // contiguous bytes of K (and of V) per slot — which DRAM serves faster than
 // separate per-head streams (a load-only probe of config 2's rows: +5% for
 // all 8 heads together). A (sequence, group) is split at the same keys for
-// each of its heads; a wave's two partial slots hold the group's HG heads
-// (AttnArgs::part_heads = HG). Shares are counted in work units (a
+// each of its heads. P groups share a work-group, one wave each: the split
+// runs over (P groups, sequence, key), so the P waves of one CU read the
+// same slots' rows of P * HG adjacent heads at about the same time (config
+// 2: 193.6 -> 189.2 us, fp8 109.2 -> 106.0 us, P = 4 against one wave per
+// work-group). A work-group's two partial slots hold its P * HG heads
+// (AttnArgs::part_heads = P * HG). Shares are counted in work units (a
 // segment's 32-key tiles plus AttnArgs::seg_cost for starting it), not in
 // keys.
 // ---------------------------------------------------------------------------
-template <typename T, int D, bool F8, int HG>
-__global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
+template <typename T, int D, bool F8, int HG, int P>
+__global__ __launch_bounds__(64 * P) void decode_grouped(AttnArgs a) {
   using L = KvTile<D, F8>;
   static_assert(HG % 2 == 0, "an even head count keeps every ring stage index a constant");
-  __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds;
+  __shared__ __attribute__((aligned(1024))) DecodeLds<D, F8> lds_of[P];
   const float vscale = F8 ? a.v_scale : 1.f;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  // Wave pw of the work-group folds head group P * grp + pw: the P waves
+  // of a work-group walk the same keys of adjacent groups.
+  const int pw = P > 1 ? (int)(threadIdx.x >> 6) : 0;
+  DecodeLds<D, F8>& lds = lds_of[pw];
   const int w = blockIdx.x;
-  const int ngroups = a.num_kv_heads / HG;
+  const int ngroups = a.num_kv_heads / (HG * P);
   // Work is counted in units: a segment (sequence, group of HG KV heads)
   // of c keys is ceil(c / 32) tiles plus a.seg_cost units for starting it
   // (its query, its slots, the ring's first tile), the latter first. Every
@@ -149,8 +157,9 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
   const uint32_t row_bytes = (uint32_t)(a.p_s0 * esize);
   const float sc = a.scale * (F8 ? a.k_scale : 1.f) * kLog2eMfma;
   const int64_t head_bytes = a.p_s1 * esize;
-  float* part_o = a.part_o + (int64_t)w * 2 * HG * G * a.head_dim;
-  float* part_lse = a.part_lse + (int64_t)w * 2 * HG * G;
+  // Partial rows of slot s: ((w * 2 + s) * P + pw) * HG * G onwards.
+  float* part_o = a.part_o + ((int64_t)w * 2 * P + pw) * HG * G * a.head_dim;
+  float* part_lse = a.part_lse + ((int64_t)w * 2 * P + pw) * HG * G;
   int ctx = decode_keys(a, seq);
   int nu = (ctx + 31) / 32 + R;  // units of each of the sequence's segments
   int u0 = (int)(gpos - before);
@@ -163,7 +172,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
     if (t_hi > t_lo) {
       const int key0 = 32 * t_lo;
       const int take = min(32 * t_hi, ctx) - key0;
-      const int h0 = grp * HG;  // the group's first KV head
+      const int h0 = (grp * P + pw) * HG;  // the group's first KV head
       if (t_lo == 0 && lane < HG) {
         // This wave holds the context's first key: the waves holding its
         // pieces, for each head of the group.
@@ -257,7 +266,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
                         (int64_t)(h0 + nw_head) * head_bytes + 16 * nw_c;
             *reinterpret_cast<u32x4_t*>(dst) = new_row;
           }
-        } else if (lane == 0 && grp == 0 && a.bad) {
+        } else if (lane == 0 && grp == 0 && pw == 0 && a.bad) {
           atomicAdd(a.bad, 1);
         }
       }
@@ -269,7 +278,7 @@ __global__ __launch_bounds__(64) void decode_grouped(AttnArgs a) {
           store_state<T, D>(st[h], static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)(h0 + h) * G * a.o_s1,
                             a.o_s1, nullptr, nullptr, 0, G, vscale);
         } else {
-          const int64_t r = ((int64_t)slot * HG + h) * G;
+          const int64_t r = ((int64_t)slot * P * HG + h) * G;
           store_state<T, D>(st[h], nullptr, 0, part_o + r * a.head_dim, part_lse + r, 1, G, vscale);
         }
       }
@@ -440,7 +449,11 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
 #define LI_DECODE_LAUNCH(T, D, F8)                                                                   \
   do {                                                                                               \
     if (balanced && a.part_heads == kDecodeHeadGroup)                                                \
-      hipLaunchKernelGGL((decode_grouped<T, D, F8, kDecodeHeadGroup>), grid, block, 0, s, a);        \
+      hipLaunchKernelGGL((decode_grouped<T, D, F8, kDecodeHeadGroup, 1>), grid, block, 0, s, a);     \
+    else if (balanced && a.part_heads == 2 * kDecodeHeadGroup)                                       \
+      hipLaunchKernelGGL((decode_grouped<T, D, F8, kDecodeHeadGroup, 2>), grid, dim3(128), 0, s, a); \
+    else if (balanced && a.part_heads == 4 * kDecodeHeadGroup)                                       \
+      hipLaunchKernelGGL((decode_grouped<T, D, F8, kDecodeHeadGroup, 4>), grid, dim3(256), 0, s, a); \
     else if (balanced) hipLaunchKernelGGL((decode_balanced<T, D, F8>), grid, block, 0, s, a);        \
     else hipLaunchKernelGGL((decode_partitioned<T, D, F8>), grid, block, 0, s, a);                   \
   } while (0)

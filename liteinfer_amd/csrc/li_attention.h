@@ -133,6 +133,13 @@ __host__ __device__ inline int prefill_row_groups(unsigned long long row_keys, u
 #define LI_DECODE_HEAD_GROUP 2
 #endif
 constexpr int kDecodeHeadGroup = LI_DECODE_HEAD_GROUP;
+// Head groups of the head-grouped decode whose waves share one work-group
+// (and so one CU), each folding the same keys of its own group: at most
+// this many, the largest power of two dividing the group count.
+#ifndef LI_DECODE_CU_GROUPS
+#define LI_DECODE_CU_GROUPS 4
+#endif
+constexpr int kDecodeCuGroups = LI_DECODE_CU_GROUPS;
 
 // Largest head_dim the general-shape kernel serves.
 constexpr int kGenericMaxHeadDim = 512;

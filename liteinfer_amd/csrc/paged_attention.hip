@@ -73,13 +73,24 @@ int balanced_waves(int num_cus) {
   return std::max(1, num_cus) * kBalancedWavesPerCu;
 }
 
-// KV heads per partial slot of the balanced split: kDecodeHeadGroup when
-// the head-grouped kernel serves the shape (num_kv_heads a multiple of the
-// group), else one. Grouping pays on 16-bit pools (config 2: 204 -> 196 us)
-// and on fp8 ones, whose scores run on the fp8 matrix cores (config 2:
-// 112.5 -> 108 us; config 4 unchanged; four heads per wave: 116 / 208 us).
+// KV heads per partial slot of the balanced split: kDecodeHeadGroup times
+// the head groups sharing a work-group when the head-grouped kernel serves
+// the shape (num_kv_heads a multiple of the group), else one. Grouping pays
+// on 16-bit pools (config 2: 204 -> 196 us) and on fp8 ones, whose scores
+// run on the fp8 matrix cores (config 2: 112.5 -> 108 us; config 4
+// unchanged; four heads per wave: 116 / 208 us).
 int balanced_part_heads(int num_kv_heads) {
-  return num_kv_heads % kDecodeHeadGroup == 0 ? kDecodeHeadGroup : 1;
+  if (num_kv_heads % kDecodeHeadGroup) return 1;
+  const int ngroups = num_kv_heads / kDecodeHeadGroup;
+  int together = 1;
+  while (together < kDecodeCuGroups && ngroups % (2 * together) == 0) together *= 2;
+  return kDecodeHeadGroup * together;
+}
+
+// Work-groups of the balanced split over `waves` waves: one wave each, or
+// one per head group sharing a work-group.
+int balanced_blocks(int waves, int part_heads) {
+  return part_heads % kDecodeHeadGroup == 0 ? waves / (part_heads / kDecodeHeadGroup) : waves;
 }
 
 // What starting a segment (its query, its slots, the ring's first tile)
@@ -89,7 +100,8 @@ int segment_cost() { return kSegmentCost; }
 
 size_t balanced_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads) {
   // Sized for either pool type (the plan calls do not know it).
-  const size_t rows = (size_t)waves * 2 * groups * balanced_part_heads(num_kv_heads);
+  const int ph = balanced_part_heads(num_kv_heads);
+  const size_t rows = (size_t)balanced_blocks(waves, ph) * 2 * groups * ph;
   return align256(rows * head_dim * sizeof(float)) + align256(rows * sizeof(float)) +
          align256((size_t)batch * num_kv_heads * 16);
 }
@@ -116,11 +128,11 @@ __global__ __launch_bounds__(256) void newest_slots_kernel(const int64_t* table,
 
 // Points a balanced launch's partial buffers and piece table into `workspace`.
 void set_balanced(AttnArgs& d, int waves, void* workspace) {
-  d.num_parts = waves;
-  d.part_len = -1;
   d.part_heads = balanced_part_heads(d.num_kv_heads);
+  d.num_parts = balanced_blocks(waves, d.part_heads);
+  d.part_len = -1;
   d.seg_cost = segment_cost();
-  const size_t rows = (size_t)waves * 2 * d.groups * d.part_heads;
+  const size_t rows = (size_t)d.num_parts * 2 * d.groups * d.part_heads;
   char* p = static_cast<char*>(workspace);
   d.part_o = reinterpret_cast<float*>(p);
   p += align256(rows * d.head_dim * sizeof(float));
@@ -285,7 +297,7 @@ int paged_decode_impl(const void* q, int64_t q_stride_seq, int64_t q_stride_head
                 "li_paged_decode: fp8 pools run on the MFMA kernel only (bf16 / fp16 queries, head_dim 128, "
                 "16-byte aligned rows)");
   const bool balanced = mfma && (num_splits == 0 || !(flags & LI_FLAG_EQUAL_SPLITS));
-  const bool grouped = balanced && balanced_part_heads(num_kv_heads) == kDecodeHeadGroup;
+  const bool grouped = balanced && balanced_part_heads(num_kv_heads) % kDecodeHeadGroup == 0;
   if (newest && newest->k) {
     // The head-grouped kernel over a 16-bit pool writes the newest rows
     // itself (16-byte aligned rows); anywhere else a write of them runs
@@ -556,6 +568,7 @@ int paged_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
       // Chunks and rows in one launch: the rows' work-groups run the
       // per-head split, which fits the prefill kernels' registers.
       d.part_heads = 1;
+      d.num_parts = waves;
       return launch_prefill_with_rows(a, d, dtype, s);
     }
     if (int rc = launch_decode_mfma(d, dtype, s)) return rc;
