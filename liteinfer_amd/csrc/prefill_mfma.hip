@@ -153,8 +153,20 @@ __device__ __forceinline__ void fold_rows_first(const AttnArgs& a, const AttnArg
   const int wg = (int)blockIdx.x;
   if (wg < row_groups) {
     const int rw = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    if (rw < kRowWaves)
-      decode_balanced_wave<T, D, F8>(d, wg * kRowWaves + rw, (int64_t)row_groups * kRowWaves, lds.rows[rw]);
+    if (rw < kRowWaves) {
+      const int waves = row_groups * kRowWaves;
+      int v = wg * kRowWaves + rw;
+      // The split runs head-major: wave v + waves / Hkv starts at about the
+      // key wave v starts at, one KV head on. The kRowWaves waves of a
+      // work-group take such shares of kRowWaves adjacent heads, so one CU
+      // reads those heads' rows of each slot together (config 3: 308-311
+      // -> 302-307 us against consecutive shares of one head).
+      if (d.num_kv_heads % kRowWaves == 0 && waves % d.num_kv_heads == 0) {
+        const int per_head = waves / d.num_kv_heads;
+        v = ((wg / per_head) * kRowWaves + rw) * per_head + wg % per_head;
+      }
+      decode_balanced_wave<T, D, F8>(d, v, (int64_t)waves, lds.rows[rw]);
+    }
     // (Every row wave's loads have landed: its folds consumed them.)
     __syncthreads();
   }
