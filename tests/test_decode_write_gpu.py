@@ -96,8 +96,9 @@ def _bits(t):
         ([2000, 1, 77, 6000], 16, 8, 64, torch.float16),  # head-grouped at head_dim 64
         ([700, 33, 1], 12, 3, 128, torch.bfloat16),  # an odd KV head count: per-head kernel, write first
         ([300, 5000, 12], 64, 4, 128, torch.bfloat16),  # 16 heads per KV head
+        ([4000, 2, 900, 33], 32, 16, 128, torch.bfloat16),  # eight head pairs: two sets of four per work-group
     ],
-    ids=["bf16-8kv", "f16-d64", "three-kv-heads", "g16"],
+    ids=["bf16-8kv", "f16-d64", "three-kv-heads", "g16", "16kv"],
 )
 def test_fused_write_equals_scatter_then_decode(contexts, heads, kv_heads, dim, dtype):
     step = _Step(contexts, heads, kv_heads, dim, dtype, seed=len(contexts))

@@ -136,6 +136,18 @@ def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads):
             assert_within(_run(b, kernel=kernel, num_splits=splits), want, 2 ** -6, 2e-3)
 
 
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(64, 16), (24, 12), (12, 6), (16, 4)])
+def test_head_groups_sharing_work_groups(num_heads, num_kv_heads):
+    """KV head counts whose pairs the head-grouped decode runs four (16),
+    two (12, 4) or one (6) to a work-group, with more than one set of
+    work-group groups where the pair count exceeds four (16, 12): long and
+    short contexts, so that work-groups cross both sequence and head-group
+    boundaries."""
+    b = PagedBatch([5000, 1, 77, 2100, 32, 9000, 640], dtype=torch.bfloat16, num_heads=num_heads,
+                   num_kv_heads=num_kv_heads, head_dim=128, num_slots=1 << 15, seed=4)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+
+
 def test_mfma_and_general_kernels_agree():
     b = PagedBatch([513, 64, 2000, 1], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128,
                    num_slots=8192, seed=4)
