@@ -31,10 +31,7 @@ __device__ __forceinline__ int kappa(int g, int e) { return (e < 4 ? 4 * g + e :
 // Keys whose slots are staged in LDS at a time. A partition chosen by the
 // policy is at most this long, so it is one chunk; a pinned split count can
 // make longer partitions, which take several.
-#ifndef LI_SLOT_CHUNK
-#define LI_SLOT_CHUNK 1024
-#endif
-constexpr int kSlotChunk = LI_SLOT_CHUNK;
+constexpr int kSlotChunk = 1024;
 
 // LDS tile layout. A tile is 32 keys; K rows then V rows, D / 8 chunks of 16
 // bytes per row. A load instruction writes lane L's 16 bytes at 16 L, so with
