@@ -107,6 +107,17 @@ def test_fused_write_equals_scatter_then_decode(contexts, heads, kv_heads, dim, 
     assert torch.equal(_bits(fused), _bits(paired))
 
 
+def test_fused_write_over_thousands_of_sequences():
+    """2,000 sequences of 1-70 keys (about ten segments per work-group):
+    every newest row lands in its slot and the attention matches the
+    scatter-then-decode pair bit for bit."""
+    rng = np.random.default_rng(13)
+    step = _Step(rng.integers(1, 71, size=2000).tolist(), seed=13, num_slots=1 << 17)
+    (fused, kp1, vp1), (paired, kp2, vp2) = _two_ways(step)
+    assert torch.equal(_bits(kp1), _bits(kp2)) and torch.equal(_bits(vp1), _bits(vp2))
+    assert torch.equal(_bits(fused), _bits(paired))
+
+
 @pytest.mark.parametrize("kernel", ["equal_splits", "generic"])
 def test_other_kernels_write_first(kernel):
     step = _Step([100, 1, 4000], seed=3)

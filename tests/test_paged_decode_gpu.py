@@ -148,6 +148,18 @@ def test_head_groups_sharing_work_groups(num_heads, num_kv_heads):
     assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
 
 
+@pytest.mark.parametrize("num_kv_heads", [8, 2])
+def test_thousands_of_short_contexts(num_kv_heads):
+    """2,500 sequences of 1-80 keys: every work-group of the balanced grid
+    walks about ten segments, and its starting sequence is found past the
+    first 64 of the batch's key counts."""
+    rng = np.random.default_rng(11)
+    ctx = rng.integers(1, 81, size=2500).tolist()
+    b = PagedBatch(ctx, dtype=torch.bfloat16, num_heads=4 * num_kv_heads, num_kv_heads=num_kv_heads,
+                   head_dim=128, num_slots=1 << 17, seed=11)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+
+
 def test_mfma_and_general_kernels_agree():
     b = PagedBatch([513, 64, 2000, 1], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128,
                    num_slots=8192, seed=4)
