@@ -51,7 +51,7 @@ from liteinfer_amd import _native  # noqa: E402
 from liteinfer_amd.attention import PagedKV, paged_attention  # noqa: E402
 from liteinfer_amd.cache.kv_cache import scatter_into  # noqa: E402
 from liteinfer_amd.paged_kernels import kv_scatter, paged_decode  # noqa: E402
-from liteinfer_amd.workloads import c3_shapes, decode_step, packed_step  # noqa: E402
+from liteinfer_amd.workloads import LLAMA_3_2_1B, c3_shapes, decode_step, packed_step  # noqa: E402
 
 METRIC = "paged-decode HBM GB/s (% of peak); prefill attn TFLOP/s; e2e output tok/s"
 HBM_PEAK_GBS = 8000.0
@@ -200,12 +200,14 @@ def _time_prefill(step, steps, warmup):
     return [a.elapsed_time(b) for a, b in marks]
 
 
-def graph_replay_us(fn, replays: int = 100, repeats: int = 5) -> float:
-    """Per-replay microseconds of `fn` captured once into a HIP graph.
+def graph_replay_us(fn, replays: int = 100, repeats: int = 5, calls: int = 1) -> float:
+    """Per-call microseconds of `fn` captured `calls` times into one HIP graph.
 
     `replays` back-to-back replays are bracketed by HIP events; the best of
     `repeats` such runs is kept (the reference's own method for its layer
-    timings). Host launch cost is out of the figure.
+    timings). A replay costs the host ~16 us to launch on this stack, so a
+    call shorter than that needs `calls` > 1 (as a model step's graph holds
+    every layer's call) for its own time to show.
     """
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -215,7 +217,8 @@ def graph_replay_us(fn, replays: int = 100, repeats: int = 5) -> float:
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        fn()
+        for _ in range(calls):
+            fn()
     graph.replay()
     torch.cuda.synchronize()
     best = float("inf")
@@ -226,7 +229,7 @@ def graph_replay_us(fn, replays: int = 100, repeats: int = 5) -> float:
             graph.replay()
         b.record()
         torch.cuda.synchronize()
-        best = min(best, a.elapsed_time(b) * 1e3 / replays)
+        best = min(best, a.elapsed_time(b) * 1e3 / (replays * calls))
     del graph
     return best
 
@@ -458,6 +461,71 @@ def cpu_baseline(seed: int = 0, device: str = "cuda", budget_s: float = 20.0, gp
     }
 
 
+# The reference's own per-call timings (NVIDIA A40, Llama-3.2-1B attention
+# geometry: 32 query / 8 KV heads, head_dim 64, bf16, block 16; captured
+# CUDA graph, best of 5), docs/benchmarks.md of the reference: decode per
+# attention call (:418-423), decode per layer at batch 1 (:1222-1228; the
+# better of its unsplit and 21-split figures), chunks over a cached prefix
+# and mixed passes (:1373-1391), whole prompts (:1418-1426). Each row:
+# (name, kind, spec, A40 microseconds).
+REFERENCE_A40_SHAPES = [
+    ("decode B=1 ctx 190", "decode", [190], 47.0),
+    ("decode B=32 ctx 190", "decode", [190] * 32, 38.0),
+    ("decode B=32 ctx 1024", "decode", [1024] * 32, 131.0),
+    ("decode B=32 ctx 2048", "decode", [2048] * 32, 253.0),
+    ("decode B=1 ctx 128", "decode", [128], 4.2),
+    ("decode B=1 ctx 1024", "decode", [1024], 5.8),
+    ("decode B=1 ctx 4096", "decode", [4096], 21.0),
+    ("decode B=1 ctx 16384", "decode", [16384], 64.6),
+    ("chunk 64 over 0", "packed", ([(64, 0)], []), 10.2),
+    ("chunk 64 over 4096", "packed", ([(64, 4096)], []), 144.8),
+    ("chunk 64 over 15000", "packed", ([(64, 15000)], []), 492.0),
+    ("chunk 512 over 0", "packed", ([(512, 0)], []), 32.6),
+    ("chunk 512 over 4096", "packed", ([(512, 4096)], []), 272.6),
+    ("chunk 512 over 15000", "packed", ([(512, 15000)], []), 945.3),
+    ("chunk 2048 over 0", "packed", ([(2048, 0)], []), 227.2),
+    ("chunk 2048 over 2048", "packed", ([(2048, 2048)], []), 629.2),
+    ("chunk 2048 over 8192", "packed", ([(2048, 8192)], []), 1939.1),
+    ("chunk 512 over 4096 beside 7 prompts of 64", "packed", ([(512, 4096)] + [(64, 0)] * 7, []), 274.9),
+    ("31 one-token rows over 2000 beside a 256 chunk", "packed", ([(256, 0)], [2000] * 31), 264.6),
+    ("prompts 1 x 4096", "packed", ([(4096, 0)], []), 802.8),
+    ("prompts 32 x 18", "packed", ([(18, 0)] * 32, []), 19.8),
+    ("prompts 32 x 128", "packed", ([(128, 0)] * 32, []), 130.4),
+    ("prompts 8 x 512", "packed", ([(512, 0)] * 8, []), 160.1),
+]
+
+
+def _reference_shapes(seed: int) -> list:
+    """This build's call time on the reference's own benchmark shapes, beside the reference's A40 figure.
+
+    Same geometry and method as the reference's tables (Llama-3.2-1B attention
+    geometry; calls captured in a graph, best of 5 runs: 20 calls per graph,
+    20 replays, so that the ~16 us a graph launch costs the host here is not
+    what a short call measures);
+    the fraction is of this GPU's roofline (8 TB/s for decode, 2.5 PF/s bf16
+    for packed passes). Other hardware: a ratio of platforms, not of kernels.
+    """
+    out = []
+    for name, kind, spec, a40_us in REFERENCE_A40_SHAPES:
+        if kind == "decode":
+            step = decode_step("custom", seed=seed, context_lens=spec, geometry=LLAMA_3_2_1B)
+            us = graph_replay_us(_decode_call(step), replays=20, calls=20)
+            work = decode_bytes(step.host_context_lens, step.geometry)
+            frac = {"frac_hbm": round(work / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        else:
+            chunks, rows = spec
+            step = packed_step("custom", seed=seed, chunks=chunks, decode_contexts=rows, geometry=LLAMA_3_2_1B,
+                               num_blocks=8192)
+            us = graph_replay_us(_prefill_call(step), replays=20, calls=20)
+            flops = prefill_flops(step.host_query_lens, step.host_context_lens, step.geometry)
+            frac = {"frac_bf16_peak": round(flops / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        out.append({"shape": name, "us": round(us, 2), "reference_a40_us": a40_us,
+                    "a40_over_this": round(a40_us / us, 2), **frac})
+        del step
+    torch.cuda.empty_cache()
+    return out
+
+
 def _traffic():
     if TRAFFIC_FILE.exists():
         try:
@@ -527,8 +595,15 @@ def main() -> int:
                         help="time only this packed prefill pass (for profiling) and print its line")
     parser.add_argument("--only-step", action="store_true",
                         help="time only config 2's fused decode step (for profiling) and print its line")
+    parser.add_argument("--only-reference-shapes", action="store_true",
+                        help="time only the reference's own benchmark shapes (Llama-3.2-1B geometry) and print them")
     args = parser.parse_args()
 
+    if args.only_reference_shapes and args.gpus == 1:
+        _native.load()
+        for row in _reference_shapes(args.seed):
+            print(json.dumps(row), flush=True)
+        return 0
     if args.only_prefill and args.gpus == 1:
         return _only_prefill(args.only_prefill, args.seed, args.steps, args.warmup)
     if args.only_step and args.gpus == 1:
@@ -720,6 +795,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         secondary["rope_kv_write_c3"] = _time_rope(1, c3_tokens, geo3)
         secondary["rope_kv_write_c2"] = _time_rope(64, 1, geo3)
+        secondary["reference_a40_shapes"] = _reference_shapes(args.seed)
         result["secondary"] = secondary
         torch.cuda.empty_cache()
         step = None

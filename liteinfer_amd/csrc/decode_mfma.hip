@@ -11,6 +11,12 @@
 namespace li {
 namespace {
 
+// Waves per (sequence, head) of the many-piece combine.
+#ifndef LI_COMBINE_WAVES
+#define LI_COMBINE_WAVES 4
+#endif
+constexpr int kCombineWaves = LI_COMBINE_WAVES;
+
 // ---------------------------------------------------------------------------
 // Partitioned decode: one wave per (sequence, KV head, partition). Serves a
 // pinned split count (the reference's equal-slice rule: partition p of a
@@ -424,6 +430,95 @@ __global__ __launch_bounds__(64) void combine_balanced(AttnArgs a) {
   }
 }
 
+// The combine for launches whose contexts are cut into many pieces (few
+// segments over the whole grid: a long context at a small batch). NW waves
+// share each (sequence, head): wave v folds pieces v, v + NW, ... in rounds
+// of 32 loaded together, as the single-wave rounds above do, and wave 0
+// merges the NW running states through LDS. A context the grid cut into
+// 130 pieces then takes two rounds per wave instead of five in a row (one
+// 4096-key context at batch 1: 23.6 -> 12.9 us a call; config 4: 339.3 ->
+// 336.1 us; 4 waves measured faster than 2 or 8 over 1-16k keys).
+template <typename T, int NW>
+__global__ __launch_bounds__(64 * NW) void combine_wide(AttnArgs a) {
+  static_assert(kMfmaMaxHeadDim <= 128, "two dims per lane");
+  constexpr int kWide = 32;
+  const int lane = threadIdx.x & 63;
+  const int v = (int)(threadIdx.x >> 6);
+  const int head = blockIdx.x % a.num_heads;
+  const int seq = blockIdx.x / a.num_heads;
+  const int G = a.groups, D = a.head_dim;
+  const int kvh = head / G, h = head % G;
+  const int keys = decode_keys(a, seq);
+  const int4 info = a.pieces[(int64_t)seq * a.num_kv_heads + kvh];
+  const int row = decode_row(a, seq);
+  T* orow = row >= 0 ? static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)head * a.o_s1 : nullptr;
+  if (keys == 0) {
+    // No key to attend to: 0 / 0, as combine_balanced writes it.
+    if (v == 0 && orow)
+      for (int d = lane; d < D; d += 64) orow[d] = li_quiet_nan<T>();
+    return;
+  }
+  const int w0 = info.x, w1 = info.y, slot0 = info.z;
+  if (w1 <= w0) return;
+  const int n = w1 - w0 + 1;
+  const int ph = a.part_heads;
+  auto row_of = [&](int j) -> int64_t {
+    return (((int64_t)(w0 + j) * 2 + (j == 0 ? slot0 : 0)) * ph + kvh % ph) * G + h;
+  };
+  const int d0 = 2 * lane;
+  const bool has = d0 < D;
+  float m = -INFINITY, wsum = 0.f;
+  float2 acc = {0.f, 0.f};
+  // This wave's pieces: v, v + NW, ...; its i-th is piece v + NW * i.
+  const int mine = n > v ? (n - v + NW - 1) / NW : 0;
+  for (int i0 = 0; i0 < mine; i0 += kWide) {
+    const int jn = min(kWide, mine - i0);
+    const float lse = lane < jn ? a.part_lse[row_of(v + NW * (i0 + lane))] : -INFINITY;
+    float2 x[kWide];
+#pragma unroll
+    for (int k = 0; k < kWide; ++k) {
+      const int j = v + NW * (i0 + min(k, jn - 1));
+      x[k] = has ? *reinterpret_cast<const float2*>(a.part_o + row_of(j) * D + d0) : float2{0.f, 0.f};
+    }
+    const float nm = fmaxf(m, li_wave_max(lse));
+    const float keep = m == -INFINITY ? 0.f : exp2f(m - nm);
+    const float wl = lane < jn ? exp2f(lse - nm) : 0.f;
+    wsum = wsum * keep + li_wave_sum(wl);
+    acc.x *= keep;
+    acc.y *= keep;
+#pragma unroll
+    for (int k = 0; k < kWide; ++k) {
+      const float wt = k < jn ? __shfl(wl, k, 64) : 0.f;
+      acc.x = fmaf(wt, x[k].x, acc.x);
+      acc.y = fmaf(wt, x[k].y, acc.y);
+    }
+    m = nm;
+  }
+  __shared__ float s_m[NW], s_w[NW];
+  __shared__ float2 s_acc[NW][64];
+  if (lane == 0) {
+    s_m[v] = m;
+    s_w[v] = wsum;
+  }
+  s_acc[v][lane] = acc;
+  __syncthreads();
+  if (v != 0 || !has || !orow) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < NW; ++u) mx = fmaxf(mx, s_m[u]);
+  float tot = 0.f;
+  float2 o = {0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < NW; ++u) {
+    const float sc = s_m[u] == -INFINITY ? 0.f : exp2f(s_m[u] - mx);
+    tot = fmaf(s_w[u], sc, tot);
+    o.x = fmaf(s_acc[u][lane].x, sc, o.x);
+    o.y = fmaf(s_acc[u][lane].y, sc, o.y);
+  }
+  const float inv = 1.f / tot;
+  *reinterpret_cast<uint32_t*>(orow + d0) = li_pack2<T>(o.x * inv, o.y * inv);
+}
+
 bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
   return aligned16(p) && (s0 * esize) % 16 == 0 && (s1 * esize) % 16 == 0;
 }
@@ -475,6 +570,20 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
 int launch_combine_balanced(const AttnArgs& a, int dtype, hipStream_t s) {
   const int64_t cblocks = (int64_t)a.batch * a.num_heads;
   if (cblocks == 0) return LI_OK;
+  // Segments (sequence, group of part_heads KV heads) against the grid's
+  // shares: fewer than one segment per kWideShare shares means most
+  // segments are cut into more than kWideShare pieces.
+  constexpr int kWideShare = 8;
+  const int64_t segments = (int64_t)a.batch * (a.num_kv_heads / std::max(a.part_heads, 1));
+  if (segments * kWideShare < a.num_parts) {
+    if (dtype == LI_BF16)
+      hipLaunchKernelGGL((combine_wide<li_bf16, kCombineWaves>), dim3((unsigned)cblocks), dim3(64 * kCombineWaves), 0,
+                         s, a);
+    else
+      hipLaunchKernelGGL((combine_wide<li_f16, kCombineWaves>), dim3((unsigned)cblocks), dim3(64 * kCombineWaves), 0,
+                         s, a);
+    return check_launch("combine_wide");
+  }
   if (dtype == LI_BF16) hipLaunchKernelGGL(combine_balanced<li_bf16>, dim3((unsigned)cblocks), dim3(64), 0, s, a);
   else hipLaunchKernelGGL(combine_balanced<li_f16>, dim3((unsigned)cblocks), dim3(64), 0, s, a);
   return check_launch("combine_balanced");

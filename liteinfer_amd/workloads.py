@@ -115,8 +115,9 @@ def _pool(geo: Geometry, num_blocks: int, dtype, device, gen):
 
 
 def decode_step(config: str, dtype=torch.bfloat16, device="cuda", seed: int = 0,
-                context_lens: list[int] | None = None, num_blocks: int | None = None) -> DecodeStep:
-    """Inputs of the c1, c2 or c4 decode step (or custom contexts at Llama-3-8B geometry)."""
+                context_lens: list[int] | None = None, num_blocks: int | None = None,
+                geometry: Geometry = LLAMA_3_8B) -> DecodeStep:
+    """Inputs of the c1, c2 or c4 decode step (or custom contexts, at `geometry`)."""
     rng = np.random.default_rng(seed)
     device = torch.device(device)
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -127,7 +128,7 @@ def decode_step(config: str, dtype=torch.bfloat16, device="cuda", seed: int = 0,
     elif config == "c4":
         geo, ctxs, blocks = LLAMA_3_8B, rng.integers(32768, 131072 + 1, size=8).tolist(), 65536
     elif config == "custom":
-        geo, ctxs = LLAMA_3_8B, list(context_lens or [])
+        geo, ctxs = geometry, list(context_lens or [])
         blocks = num_blocks or -(-sum(ctxs) // BLOCK_SIZE) + len(ctxs)
     else:
         raise ValueError(f"unknown decode config {config!r}")

@@ -41,6 +41,16 @@ def test_decode_rows_beside_chunks_in_one_launch():
     _fp32_close(_run(b), b.oracle())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_long_rows_beside_a_chunk_cut_into_many_pieces(dtype):
+    """Two one-query rows over 20,000 and 9,000 keys beside a 64-query chunk:
+    the rows' split cuts each (row, KV head) into many pieces, which the
+    many-piece combine (several waves per head) folds."""
+    b = PagedBatch([20000, 300, 9000], [1, 64, 1], dtype=dtype, num_heads=32, num_kv_heads=8, head_dim=128,
+                   num_slots=1 << 15, seed=21)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+
+
 @pytest.mark.parametrize("block_q", [1, 4, 16, 32])
 def test_the_answer_does_not_depend_on_the_query_block(block_q):
     b = PagedBatch([100, 16, 47, 9], [33, 16, 15, 1], num_slots=2048)
