@@ -110,17 +110,22 @@ __global__ __launch_bounds__(64 * P) void decode_grouped(AttnArgs a) {
   // wave takes an equal run of units, so a wave that meets more segments
   // folds fewer tiles, and pieces start and end on tile boundaries.
   const int R = a.seg_cost;
-  auto units_of = [&](int sq) -> int64_t {
-    const int c = decode_keys(a, sq);
+  // The first 64 sequences' key counts stay in registers (lane s holds
+  // sequence s's): the scans below and the walk from segment to segment
+  // read them without another round trip, which small launches feel.
+  const int keys0 = lane < a.batch ? decode_keys(a, lane) : 0;
+  // Sequence sq's key count, sq the same on every lane.
+  auto keys_at = [&](int sq) -> int { return sq < 64 ? __shfl(keys0, sq, 64) : decode_keys(a, sq); };
+  // Lane's sequence s0 + lane (0 past the batch).
+  auto lane_units = [&](int s0) -> int64_t {
+    const int sq = s0 + lane;
+    const int c = s0 == 0 ? keys0 : (sq < a.batch ? decode_keys(a, sq) : 0);
     return c > 0 ? (int64_t)((c + 31) / 32 + R) : 0;
   };
   int64_t total;
   {
     int64_t t = 0;
-    for (int s0 = 0; s0 < a.batch; s0 += 64) {
-      const int sq = s0 + lane;
-      t += sq < a.batch ? units_of(sq) : 0;
-    }
+    for (int s0 = 0; s0 < a.batch; s0 += 64) t += lane_units(s0);
     total = wave_sum_i64(t) * ngroups;
   }
   const int64_t share = (total + a.num_parts - 1) / a.num_parts;
@@ -137,8 +142,7 @@ __global__ __launch_bounds__(64 * P) void decode_grouped(AttnArgs a) {
   int seq = 0;
   int64_t before = 0;  // units of the sequences before `seq`
   for (int s0 = 0; s0 < a.batch; s0 += 64) {
-    const int sq = s0 + lane;
-    const int64_t c = sq < a.batch ? units_of(sq) : 0;
+    const int64_t c = lane_units(s0);
     int64_t incl = c;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -166,7 +170,7 @@ __global__ __launch_bounds__(64 * P) void decode_grouped(AttnArgs a) {
   // Partial rows of slot s: ((w * 2 + s) * P + pw) * HG * G onwards.
   float* part_o = a.part_o + ((int64_t)w * 2 * P + pw) * HG * G * a.head_dim;
   float* part_lse = a.part_lse + ((int64_t)w * 2 * P + pw) * HG * G;
-  int ctx = decode_keys(a, seq);
+  int ctx = keys_at(seq);
   int nu = (ctx + 31) / 32 + R;  // units of each of the sequence's segments
   int u0 = (int)(gpos - before);
   bool first_segment = true;
@@ -294,15 +298,15 @@ __global__ __launch_bounds__(64 * P) void decode_grouped(AttnArgs a) {
     u0 = 0;
     before += nu;
     ++seq;
-    while (seq < a.batch && decode_keys(a, seq) == 0) ++seq;
+    while (seq < a.batch && keys_at(seq) == 0) ++seq;
     if (seq >= a.batch) {
       if (++grp == ngroups) break;
       seq = 0;
       before = 0;
-      while (seq < a.batch && decode_keys(a, seq) == 0) ++seq;
+      while (seq < a.batch && keys_at(seq) == 0) ++seq;
       if (seq >= a.batch) break;
     }
-    ctx = decode_keys(a, seq);
+    ctx = keys_at(seq);
     nu = (ctx + 31) / 32 + R;
   }
 }
