@@ -50,6 +50,17 @@ struct AttnArgs {
                  // (prefill_pp_rows) the number of work-groups that fold the one-query rows first
   int row_groups_max;  // prefill_pp_rows: most work-groups that may fold the rows, min(grid, d.num_parts /
                        // kRowWaves) (0: the one-query rows are not in the launch)
+  // MFMA prefill of a pass too small to fill the grid (prefill_pp only):
+  // prefill_order may cut a block's fully visible key stages into pieces,
+  // one work-list entry each, consecutive; each piece folds its stages and
+  // stores its rows unnormalised with their running maximum and sum, and
+  // prefill_merge folds the pieces into the output. split_ok == 0: never.
+  int split_ok;
+  int split_target;  // units (entries x KV heads) the pieces should make in all
+  int4* work_range;  // per entry {first 64-key stage, end stage, piece, pieces}
+  float* split_o;    // [entry * num_kv_heads + KV head][256 rows][head_dim]
+  float* split_ml;   // [entry * num_kv_heads + KV head][256 rows]{running maximum, sum}
+  int* split_first;  // the first entry of each split block; their count: queue[kPrefillQueues + 2]
   // fp8 (e4m3) pools: kp / vp hold K / k_scale and V / v_scale, one byte per
   // element (pool strides in bytes); the MFMA kernels only. Other pools hold
   // the query's dtype and ignore the scales.
@@ -68,6 +79,19 @@ struct AttnArgs {
 
 // Work queues of the persistent MFMA prefill grid (one per XCD).
 constexpr int kPrefillQueues = 8;
+// Rows of a prefill unit (8 waves of 32), and the fewest 64-key stages a
+// piece of a split unit holds.
+constexpr int kPrefillUnitRows = 256;
+constexpr int kSplitMinStages = 8;
+constexpr int kSplitMaxPieces = 32;
+// Split blocks a pass cut to at most `target` units can hold: each has two
+// pieces or more, and the pieces are at most target / num_kv_heads entries.
+inline int prefill_split_blocks_cap(int target, int num_kv_heads) {
+  return (target + 2 * num_kv_heads - 1) / (2 * num_kv_heads);
+}
+// Ints of a prefill launch's queue array: the per-XCD unit counters, the
+// listed entries, the row work-groups, the split blocks.
+constexpr int kPrefillQueueInts = kPrefillQueues + 3;
 
 // Decode waves per work-group of a prefill launch that folds the pass's
 // one-query rows first (prefill_pp_rows, prefill_mfma_rows). (Eight waves

@@ -463,11 +463,40 @@ extern "C" int li_paged_decode_noalloc(const void* q, int64_t q_stride_seq, int6
                            scratch, (size_t)LI_DECODE_NOALLOC_SCRATCH_BYTES, dtype, dtype, 1.f, 1.f, flags, stream);
 }
 
+// The persistent prefill grid: one work-group per CU, a multiple of the
+// queue count.
+int prefill_grid() { return (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues; }
+
+// Whether a pass of `batch` sequences may be split (prefill_order cuts the
+// blocks of a pass that leaves most of the grid idle): at least one block
+// per sequence and KV head must leave half the grid free. The workspace of
+// such a batch holds the pieces' partial rows: one 256-row slot per unit of
+// the grid (a split pass lists at most grid / num_kv_heads entries).
+bool prefill_split_room(int batch, int num_kv_heads) {
+  return batch <= 1024 && (int64_t)batch * num_kv_heads * 2 <= prefill_grid();
+}
+
+size_t prefill_split_bytes(int batch, int num_kv_heads, int head_dim) {
+  if (!prefill_split_room(batch, num_kv_heads)) return 0;
+  const size_t rows = (size_t)prefill_grid() * kPrefillUnitRows;
+  return align256(rows * head_dim * sizeof(float)) + align256(rows * 2 * sizeof(float)) +
+         align256((size_t)prefill_split_blocks_cap(prefill_grid(), num_kv_heads) * sizeof(int));
+}
+
+// Work-list entries: the blocks, and a split pass's pieces.
+size_t prefill_list_entries(int batch, int num_kv_heads, int max_context) {
+  return prefill_work_entries(batch, max_context) +
+         (prefill_split_room(batch, num_kv_heads) ? (size_t)cdiv(prefill_grid(), num_kv_heads) : 0);
+}
+
 // Workspace of the MFMA prefill path: the balanced decode kernel's partials
-// for the one-query sequences, then the prefill work list and its queues.
+// for the one-query sequences, then the prefill work list, its queues, the
+// entries' stage ranges and a split pass's partial rows.
 size_t prefill_workspace(int waves, int groups, int head_dim, int batch, int num_kv_heads, int max_context) {
-  return balanced_workspace(waves, groups, head_dim, batch, num_kv_heads) +
-         align256(prefill_work_entries(batch, max_context) * sizeof(int4)) + align256((kPrefillQueues + 2) * sizeof(int));
+  const size_t entries = prefill_list_entries(batch, num_kv_heads, max_context);
+  return balanced_workspace(waves, groups, head_dim, batch, num_kv_heads) + align256(entries * sizeof(int4)) +
+         align256(kPrefillQueueInts * sizeof(int)) + align256(entries * sizeof(int4)) +
+         prefill_split_bytes(batch, num_kv_heads, head_dim);
 }
 
 extern "C" int li_paged_prefill_plan(int batch, int num_heads, int num_kv_heads, int head_dim, int max_context,
@@ -555,10 +584,29 @@ int paged_prefill_impl(const void* q, int64_t q_stride_tok, int64_t q_stride_hea
     const size_t need = prefill_workspace(waves, a.groups, head_dim, batch, num_kv_heads, max_context);
     if (!workspace || workspace_bytes < need)
       return fail(LI_EWORKSPACE, "li_paged_prefill: workspace of %zu bytes given, %zu needed", workspace_bytes, need);
-    a.work = reinterpret_cast<int4*>(static_cast<char*>(workspace) +
-                                    balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads));
-    a.queue = reinterpret_cast<int*>(reinterpret_cast<char*>(a.work) +
-                                     align256(prefill_work_entries(batch, max_context) * sizeof(int4)));
+    const size_t entries = prefill_list_entries(batch, num_kv_heads, max_context);
+    char* wp = static_cast<char*>(workspace) + balanced_workspace(waves, a.groups, head_dim, batch, num_kv_heads);
+    a.work = reinterpret_cast<int4*>(wp);
+    wp += align256(entries * sizeof(int4));
+    a.queue = reinterpret_cast<int*>(wp);
+    wp += align256(kPrefillQueueInts * sizeof(int));
+    // A pass that would leave at least half the grid idle, over a 16-bit
+    // pool (the ping-pong kernel), may be split into pieces.
+    const int block_q = kPrefillUnitRows / a.groups;
+    const int64_t units_max = (int64_t)batch * num_kv_heads * cdiv(max_query_len, block_q);
+    // (A context under 2 x kSplitMinStages stages has no block to cut.)
+    if (!a.kv_fp8 && prefill_split_room(batch, num_kv_heads) && units_max * 2 <= prefill_grid() &&
+        max_context >= 2 * kSplitMinStages * 64) {
+      a.split_ok = 1;
+      a.split_target = prefill_grid();
+      a.work_range = reinterpret_cast<int4*>(wp);
+      wp += align256(entries * sizeof(int4));
+      a.split_o = reinterpret_cast<float*>(wp);
+      wp += align256((size_t)prefill_grid() * kPrefillUnitRows * head_dim * sizeof(float));
+      a.split_ml = reinterpret_cast<float*>(wp);
+      wp += align256((size_t)prefill_grid() * kPrefillUnitRows * 2 * sizeof(float));
+      a.split_first = reinterpret_cast<int*>(wp);
+    }
     if (flags & LI_FLAG_PREFILL_ONLY) return launch_prefill_mfma(a, dtype, s);
     AttnArgs d = a;
     d.block_q = 1;

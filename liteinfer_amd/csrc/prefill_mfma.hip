@@ -620,6 +620,7 @@ struct PpLds {
   int unit;
   int rows[3];  // the unit's first token + q0, its query count, first head
   int4 entry;   // the work-list entry of `unit`
+  int4 range;   // its stage range and piece ({0, all, 0, 1} for a whole block)
 };
 
 
@@ -635,7 +636,7 @@ union PpShared {
 // first work-groups fold the pass's one-query rows first (the balanced
 // decode split, AttnArgs `d`, over kRowWaves waves of each of them; their
 // count was written by prefill_order), then join the queues.
-template <typename T, int D, bool kRows>
+template <typename T, int D, bool kRows, bool kSplit>
 __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   __shared__ __attribute__((aligned(1024))) PpShared<D> lds;
   const unsigned wg = blockIdx.x;
@@ -675,6 +676,15 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   // Work-list entry of unit u ({-1, ...} for a unit past the listed ones,
   // without reading the list there).
   auto entry_of = [&](int u) -> int4 { return u < units ? a.work[u / heads_per_queue] : int4{-1, 0, 0, 0}; };
+  // Its stage range and piece: a whole block unless prefill_order split it.
+  // (Only the kSplit instantiation, launched for passes the host allows to
+  // be split, reads ranges: the other's key loop is the same code as if no
+  // pass were ever split.)
+  auto range_of = [&](int u) -> int4 {
+    if constexpr (kSplit) return u < units ? a.work_range[u / heads_per_queue] : int4{0, 0x7fffffff, 0, 1};
+    return int4{0, 0x7fffffff, 0, 1};
+  };
+  int4& s_range = lds.pp.range;
   // A listed block always has queries of its own (prefill_order lists only
   // those); anything else is skipped rather than folded.
   auto block_ok = [&](const int4& e) -> bool {
@@ -685,6 +695,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     const int u = atomicAdd(&a.queue[qi], 1);
     s_unit = u;
     s_entry = entry_of(u);
+    if constexpr (kSplit) s_range = range_of(u);
   }
   int next_unit = 0;  // tid 0: the unit claimed for after this one
   // The unit's queries (the softmax scale times log2 e folded in, rounded
@@ -701,7 +712,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   int first_slots[kSlotsPer];
   Frag qf[2][kSteps];
   bool have = false;
-  auto fetch_inputs = [&](const int4& e, int u, bool slots, bool queries) __attribute__((always_inline)) {
+  auto fetch_inputs = [&](const int4& e, int u, int kbeg_, bool slots, bool queries) __attribute__((always_inline)) {
     const int seq_ = e.x / a.num_qblocks, qb_ = e.x % a.num_qblocks;
     const int nblk_ = (e.z + bq - 1) / bq;
     const int q1_ = e.z - (nblk_ - 1 - qb_) * bq;
@@ -711,7 +722,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     const int64_t* srow_ = a.st + (int64_t)seq_ * a.st_s;
     if (slots) {
 #pragma unroll
-      for (int r = 0; r < kSlotsPer; ++r) first_slots[r] = (int)srow_[min(tid + r * 64 * W, kend_ - 1)];
+      for (int r = 0; r < kSlotsPer; ++r) first_slots[r] = (int)srow_[min(kbeg_ + tid + r * 64 * W, kend_ - 1)];
     }
     if (!queries) return;
 #pragma unroll
@@ -747,6 +758,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
       const int u = atomicAdd(&a.queue[qi], 1);
       s_unit = u;
       s_entry = entry_of(u);
+      if constexpr (kSplit) s_range = range_of(u);
     }
     have = false;
     continue;
@@ -766,7 +778,15 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   const int ctx = entry.w;
   const int pos0 = ctx - nq;
   const int kend = pos0 + q1;
-  const int ns = (kend + kStageKeys - 1) / kStageKeys;  // 64-key stages
+  // The unit's 64-key stages: the block's [0, ceil(kend / 64)), or a
+  // piece's part of them. Stage numbers below count from the unit's first
+  // (key kbeg); the slot ring holds key kbeg + i at entry i % kSlotRing.
+  const int4 range = kSplit ? int4{__builtin_amdgcn_readfirstlane(s_range.x), __builtin_amdgcn_readfirstlane(s_range.y),
+                                   __builtin_amdgcn_readfirstlane(s_range.z), __builtin_amdgcn_readfirstlane(s_range.w)}
+                            : int4{0, 0x7fffffff, 0, 1};
+  const int kbeg = range.x * kStageKeys;
+  const int ns = min(range.y, (kend + kStageKeys - 1) / kStageKeys) - range.x;
+  const bool piece = kSplit && range.w > 1;  // stores partial rows for prefill_merge
   // The next unit is claimed a few stages before this one ends, so the
   // atomic's round trip is hidden, yet late enough that a work-group that
   // finishes early still takes the heaviest unit left.
@@ -778,18 +798,21 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     s_rows[2] = kvh * G;
   }
 
-  const int64_t* srow = a.st + (int64_t)seq * a.st_s;
-  fetch_inputs(entry, unit, !have, true);
+  fetch_inputs(entry, unit, kbeg, !have, true);
+  // From here keys count from the unit's first (kbeg): its slots, the
+  // rows' last visible keys and the stages' first keys.
+  const int64_t* srow = a.st + (int64_t)seq * a.st_s + kbeg;
+  const int kend_u = kend - kbeg;
   int pos[2];
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int row = 32 * w + 16 * nb + n;
     const int ql = row / G;
     const bool real = row < bq * G && q0 + ql < q1;
-    pos[nb] = real ? pos0 + q0 + ql : kend;
+    pos[nb] = real ? pos0 + q0 + ql - kbeg : kend_u;
   }
-  const int lim[2] = {min(pos[0], kend - 1), min(pos[1], kend - 1)};
-  const int lim_lo = min(pos0 + q0, kend - 1);
+  const int lim[2] = {min(pos[0], kend_u - 1), min(pos[1], kend_u - 1)};
+  const int lim_lo = min(pos0 + q0 - kbeg, kend_u - 1);
   // A wave whose 32 rows are all padding only loads stages and waits at the
   // barriers.
   const bool idle = 32 * w >= (q1 - q0) * G;
@@ -824,7 +847,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   // Slot ring: entry k % kSlotRing holds key k's slot (keys past the block's
   // last one repeat it, so every load reads a real row).
   auto stage_slots_loaders = [&](int k0, int count) {  // waves 0-3
-    for (int i = tid; i < count; i += 256) sl[(k0 + i) % kSlotRing] = (int)srow[min(k0 + i, kend - 1)];
+    for (int i = tid; i < count; i += 256) sl[(k0 + i) % kSlotRing] = (int)srow[min(k0 + i, kend_u - 1)];
   };
   using Slots = uint32_t[2 * L::kInsts / W];
   auto fire = [&](int buf, const Slots& slot) {
@@ -1064,8 +1087,11 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   lds_barrier();
   // tid 0 reads the next unit's work-list entry (its id came back from the
   // claim above) while the last P V runs.
-  int4 next_entry{-1, 0, 0, 0};
-  if (tid == 0) next_entry = entry_of(next_unit);
+  int4 next_entry{-1, 0, 0, 0}, next_range{0, 0x7fffffff, 0, 1};
+  if (tid == 0) {
+    next_entry = entry_of(next_unit);
+    if constexpr (kSplit) next_range = range_of(next_unit);
+  }
   if (!idle) {
     Frag vf[2][kBlk];
     read_v(lds_addr(vst[(ns - 1) % kPpRing]) - lds_addr(vst[0]), vf);
@@ -1076,6 +1102,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   if (tid == 0) {
     s_unit = next_unit;
     s_entry = next_entry;
+    if constexpr (kSplit) s_range = next_range;
   }
   lds_barrier();
   {
@@ -1085,9 +1112,30 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     const int4 ne{__builtin_amdgcn_readfirstlane(s_entry.x), __builtin_amdgcn_readfirstlane(s_entry.y),
                   __builtin_amdgcn_readfirstlane(s_entry.z), __builtin_amdgcn_readfirstlane(s_entry.w)};
     have = nu < units && block_ok(ne);
-    if (have) fetch_inputs(ne, nu, true, false);
+    if (have) fetch_inputs(ne, nu, kSplit ? __builtin_amdgcn_readfirstlane(s_range.x) * kStageKeys : 0, true, false);
   }
 
+  if (kSplit && piece) {
+    // A piece of a split block: its rows unnormalised, with their running
+    // maximum and sum of weights, for prefill_merge (every row, padding
+    // included; the merge writes only the block's real ones).
+    if (!idle) {
+      int el = lane;
+      asm volatile("" : "+v"(el));
+      const int en = el & 15, eg = el >> 4;
+      const int64_t slot = (int64_t)(unit / heads_per_queue) * a.num_kv_heads + kvh;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int r = 32 * w + 16 * nb + en;
+        float* orow = a.split_o + (slot * kMinRows + r) * D + 4 * eg;
+#pragma unroll
+        for (int blk = 0; blk < kBlk; ++blk) *reinterpret_cast<floatx4_t*>(orow + 16 * blk) = acc[nb][blk];
+        if (eg == 0)
+          *reinterpret_cast<float2*>(a.split_ml + (slot * kMinRows + r) * 2) = float2{m[nb], acc[nb][kBlk][0]};
+      }
+    }
+    continue;
+  }
   // The output rows, normalised. A lane holds 8-byte pieces of its row 32
   // bytes apart, so stored as they are every store instruction would write
   // 16 rows' 32-byte pieces; instead each wave stages its 32 rows in its own
@@ -1143,9 +1191,9 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   }  // units
 }
 
-template <typename T, int D>
+template <typename T, int D, bool kSplit>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp(AttnArgs a) {
-  prefill_pp_body<T, D, false>(a, a);
+  prefill_pp_body<T, D, false, kSplit>(a, a);
 }
 
 // A packed pass's chunks and one-query rows in one launch: the first
@@ -1153,10 +1201,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // each), while the others start on the chunks; each joins the chunks'
 // queues when its rows are done. The rows stream K/V from HBM while the
 // chunks keep the matrix cores busy, instead of one waiting for the other.
-template <typename T, int D>
+template <typename T, int D, bool kSplit>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp_rows(AttnArgs a,
                                                                                                   AttnArgs d) {
-  prefill_pp_body<T, D, true>(a, d);
+  prefill_pp_body<T, D, true, kSplit>(a, d);
 }
 
 // Work list of the prefill grid: every non-empty query block
@@ -1199,6 +1247,74 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   const int4 c_e = tid < a.batch ? info_of(tid) : int4{0, 0, 0, 0};
   int c_t = 0;
   const int c_nb = tid < a.batch ? blocks_of(c_e, &c_t) : 0;
+  // (One-query rows in the launch keep the pass whole: their work-groups'
+  // count is decided below.)
+  const bool has_rows = __syncthreads_or(tid < a.batch && c_e.y == 1 && a.single_query_elsewhere);
+  if (a.split_ok && !has_rows) {
+    // A pass too small to fill the grid (the host allows this only for a
+    // batch of at most 1024 sequences, so thread i holds sequence i): each
+    // block's fully visible stages -- wholly before its first query -- are
+    // cut into up to f pieces of at least kSplitMinStages stages, f the
+    // grid's units over the blocks' units. The last piece also takes the
+    // stages its queries mask, so every piece's every row sees a key. A
+    // block's pieces are consecutive entries, in sequence order.
+    __shared__ int s_blocks, s_split;
+    __shared__ int s_wave[1024 / 64];
+    if (tid == 0) {
+      s_blocks = 0;
+      s_split = 0;
+    }
+    __syncthreads();
+    if (c_nb > 0) atomicAdd(&s_blocks, c_nb);
+    __syncthreads();
+    const int f = max(1, a.split_target / max(1, s_blocks * a.num_kv_heads));
+    const int bq = a.block_q;
+    // Block qb of this thread's sequence: its stage count and its pieces.
+    auto cut = [&](int qb, int* ns, int* vis) -> int {
+      const int nq = c_e.y, ctx = c_e.z;
+      const int nblk = (nq + bq - 1) / bq;
+      const int q1 = nq - (nblk - 1 - qb) * bq;
+      const int q0 = max(q1 - bq, 0);
+      const int pos0 = ctx - nq;
+      *ns = (pos0 + q1 + kStageKeys - 1) / kStageKeys;
+      *vis = (pos0 + q0 + 1) / kStageKeys;
+      return max(1, min(min(f, kSplitMaxPieces), *vis / kSplitMinStages));
+    };
+    int mine = 0;
+    for (int i = 0; i < c_nb; ++i) {
+      int ns, vis;
+      mine += cut(c_nb - 1 - i, &ns, &vis);
+    }
+    // Exclusive prefix of `mine` over the threads.
+    const int lane = tid & 63;
+    int incl = mine;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int up = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += up;
+    }
+    if (lane == 63) s_wave[tid >> 6] = incl;
+    __syncthreads();
+    int at = incl - mine;
+    for (int v = 0; v < (tid >> 6); ++v) at += s_wave[v];
+    for (int i = 0; i < c_nb; ++i) {
+      const int qb = c_nb - 1 - i;
+      int ns, vis;
+      const int p = cut(qb, &ns, &vis);
+      const int per = vis / p;
+      if (p > 1) a.split_first[atomicAdd(&s_split, 1)] = at;
+      for (int k = 0; k < p; ++k, ++at) {
+        a.work[at] = int4{tid * a.num_qblocks + qb, c_e.x, c_e.y, c_e.z};
+        a.work_range[at] = int4{k * per, k + 1 < p ? (k + 1) * per : ns, k, p};
+      }
+    }
+    if (tid < kPrefillQueues) a.queue[tid] = 0;
+    if (tid == 1023) a.queue[kPrefillQueues] = at;  // the last thread's end: every entry listed
+    if (tid == 0 && a.row_groups_max > 0) a.queue[kPrefillQueues + 1] = 0;  // no rows to fold first
+    __syncthreads();
+    if (tid == 0) a.queue[kPrefillQueues + 2] = s_split;
+    return;
+  }
   if (tid < kOrderBins) hist[tid] = 0;
   if (tid == 0) {
     max_tiles = 0;
@@ -1254,7 +1370,10 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   __syncthreads();
   auto place = [&](int sq, const int4& e, int nb, int t) {
     const int at = atomicAdd(&hist[kOrderBins - 1 - (t >> shift)], nb);
-    for (int i = 0; i < nb; ++i) a.work[at + i] = int4{sq * a.num_qblocks + (nb - 1 - i), e.x, e.y, e.z};
+    for (int i = 0; i < nb; ++i) {
+      a.work[at + i] = int4{sq * a.num_qblocks + (nb - 1 - i), e.x, e.y, e.z};
+      if (a.split_ok) a.work_range[at + i] = int4{0, 0x7fffffff, 0, 1};  // whole blocks
+    }
   };
   if (c_nb > 0) place(tid, c_e, c_nb, c_t);
   for (int sq = tid + 1024; sq < a.batch; sq += 1024) {
@@ -1268,6 +1387,7 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   // The persistent grid's queues start empty for this launch.
   if (tid < kPrefillQueues) a.queue[tid] = 0;
   if (tid == 0) a.queue[kPrefillQueues] = max_tiles;
+  if (tid == 0 && a.split_ok) a.queue[kPrefillQueues + 2] = 0;  // no block split
   if (a.row_groups_max > 0) {
     // prefill_pp_rows: how many work-groups fold the one-query rows first.
     // The rows' K/V bytes against the chunks' flops (visible causal pairs),
@@ -1296,6 +1416,89 @@ __global__ __launch_bounds__(1024) void prefill_order(AttnArgs a) {
   }
 }
 
+// Folds the pieces of each split block into its output rows: out =
+// sum_k 2^(m_k - M) o_k / sum_k 2^(m_k - M) l_k over its pieces k, M their
+// largest running maximum (the fold of partial softmaxes, in the log2
+// domain the kernels keep their scores in). Work-group (split block i, KV
+// head, chunk of kMergeRows rows); D / 4 lanes per row, a float4 of it
+// each; lane j of a row reads the maximum and sum of pieces j, j + D / 4,
+// ...; rows of padding are skipped.
+template <int D>
+constexpr int merge_rows() { return 256 / (D / 4); }
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prefill_merge(AttnArgs a) {
+  constexpr int kLanes = D / 4;  // per row
+  constexpr int kRows = merge_rows<D>();
+  constexpr int kPer = (kSplitMaxPieces + kLanes - 1) / kLanes;  // pieces' (m, l) per lane
+  const int chunks = kMinRows / kRows;
+  const int i = (int)(blockIdx.x / (unsigned)(a.num_kv_heads * chunks));
+  const int kvh = (int)(blockIdx.x / (unsigned)chunks % (unsigned)a.num_kv_heads);
+  const int chunk = (int)(blockIdx.x % (unsigned)chunks);
+  if (i >= a.queue[kPrefillQueues + 2]) return;
+  const int e = a.split_first[i];
+  const int p = a.work_range[e].w;
+  const int4 en = a.work[e];
+  const int bq = a.block_q, G = a.groups;
+  const int qb = en.x % a.num_qblocks;
+  const int nq = en.z;
+  const int nblk = (nq + bq - 1) / bq;
+  const int q1 = nq - (nblk - 1 - qb) * bq;
+  const int q0 = max(q1 - bq, 0);
+  const int nvalid = q1 - q0;
+  const int j = (int)threadIdx.x % kLanes;
+  const int row = chunk * kRows + (int)threadIdx.x / kLanes;
+  if (row >= nvalid * G) return;
+  auto slot_of = [&](int k) -> int64_t { return ((int64_t)(e + k) * a.num_kv_heads + kvh) * kMinRows + row; };
+  float mk[kPer], lk[kPer];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    const int k = j + kLanes * t;
+    const float2 ml = k < p ? *reinterpret_cast<const float2*>(a.split_ml + slot_of(k) * 2) : float2{-INFINITY, 0.f};
+    mk[t] = ml.x;
+    lk[t] = ml.y;
+    mx = fmaxf(mx, ml.x);
+  }
+#pragma unroll
+  for (int off = 1; off < kLanes; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  float tot = 0.f;
+#pragma unroll
+  for (int t = 0; t < kPer; ++t) {
+    mk[t] = mk[t] == -INFINITY ? 0.f : exp2f(mk[t] - mx);  // piece j + kLanes t's weight
+    tot = fmaf(mk[t], lk[t], tot);
+  }
+#pragma unroll
+  for (int off = 1; off < kLanes; off <<= 1) tot += __shfl_xor(tot, off, 64);
+  const int d = 4 * j;
+  const int base = (int)threadIdx.x - j;  // the row's first lane
+  floatx4_t o = {0.f, 0.f, 0.f, 0.f};
+  for (int k0 = 0; k0 < p; k0 += 8) {
+    floatx4_t x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      x[u] = k0 + u < p ? *reinterpret_cast<const floatx4_t*>(a.split_o + slot_of(k0 + u) * D + d)
+                        : floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      float wt = 0.f;
+#pragma unroll
+      for (int t = 0; t < kPer; ++t) {
+        const float w_t = __shfl(mk[t], (base + k % kLanes) & 63, 64);
+        if (k / kLanes == t) wt = w_t;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = fmaf(wt, x[u][c], o[c]);
+    }
+  }
+  const float inv = 1.f / tot;
+  T* orow = static_cast<T*>(a.out) + (int64_t)(en.y + q0 + row / G) * a.o_s0 +
+            (int64_t)(kvh * G + row % G) * a.o_s1 + d;
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<u32x2_t*>(orow) = u32x2_t{li_pack2<T>(o[0] * inv, o[1] * inv), li_pack2<T>(o[2] * inv, o[3] * inv)};
+}
+
 bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
   return aligned16(p) && (s0 * esize) % 16 == 0 && (s1 * esize) % 16 == 0;
 }
@@ -1320,6 +1523,8 @@ bool prefill_mfma_applies(const AttnArgs& a, int dtype) {
 
 // `rows`: the one-query rows' decode split to run in the same launch
 // (prefill_pp_rows), or null.
+static int launch_prefill_merge(const AttnArgs& a, int dtype, hipStream_t s);
+
 template <int W>
 static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const AttnArgs* rows) {
   a.block_q = 32 * W / a.groups;
@@ -1328,11 +1533,15 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
   if (units == 0) return LI_OK;
   if ((size_t)a.batch * a.num_qblocks > prefill_work_entries(a.batch, a.max_context))
     return fail(LI_EINVAL, "prefill: %d query blocks per sequence exceed the planned work list", a.num_qblocks);
+  static_assert(kMinRows == kPrefillUnitRows, "a prefill unit's rows");
+  if (a.split_ok && (a.block_q != kPrefillUnitRows / a.groups || a.kv_fp8 || a.batch > 1024))
+    return fail(LI_EINVAL, "prefill: a split pass needs the ping-pong kernel's blocks");
   // One work-group per CU (its LDS and registers fill one), a multiple of
   // the queue count so every queue has work-groups, and never more than
   // there can be units (the rows' work-groups aside).
   int64_t grid = (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues;
-  if (!rows) grid = std::min<int64_t>(grid, (units + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues);
+  if (!rows && !a.split_ok)
+    grid = std::min<int64_t>(grid, (units + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues);
   // The rows' waves must fit the workspace's partial slots as well as the
   // grid: the one cap both prefill_order's rule and the kernel's clamp use.
   a.row_groups_max = rows ? prefill_row_cap(grid, rows->num_parts) : 0;
@@ -1350,27 +1559,60 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
     return launch_combine_balanced(*rows, dtype, s);
   }
   if (rows) {
+#define LI_PP_ROWS(T, D)                                                                            \
+  do {                                                                                              \
+    if (a.split_ok) hipLaunchKernelGGL((prefill_pp_rows<T, D, true>), g, block, 0, s, a, *rows);    \
+    else hipLaunchKernelGGL((prefill_pp_rows<T, D, false>), g, block, 0, s, a, *rows);              \
+  } while (0)
     if (dtype == LI_BF16) {
-      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp_rows<li_bf16, 128>), g, block, 0, s, a, *rows);
-      else hipLaunchKernelGGL((prefill_pp_rows<li_bf16, 64>), g, block, 0, s, a, *rows);
+      if (a.head_dim == 128) LI_PP_ROWS(li_bf16, 128);
+      else LI_PP_ROWS(li_bf16, 64);
     } else {
-      if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp_rows<li_f16, 128>), g, block, 0, s, a, *rows);
-      else hipLaunchKernelGGL((prefill_pp_rows<li_f16, 64>), g, block, 0, s, a, *rows);
+      if (a.head_dim == 128) LI_PP_ROWS(li_f16, 128);
+      else LI_PP_ROWS(li_f16, 64);
     }
+#undef LI_PP_ROWS
     if (int rc = check_launch("prefill_pp_rows")) return rc;
+    if (int rc = launch_prefill_merge(a, dtype, s)) return rc;
     return launch_combine_balanced(*rows, dtype, s);
   }
   if (a.kv_fp8) {
     if (dtype == LI_BF16) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true>), g, block, 0, s, a);
     else hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true>), g, block, 0, s, a);
-  } else if (dtype == LI_BF16) {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_bf16, 128>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_pp<li_bf16, 64>), g, block, 0, s, a);
   } else {
-    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_pp<li_f16, 128>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_pp<li_f16, 64>), g, block, 0, s, a);
+#define LI_PP(T, D)                                                                                 \
+  do {                                                                                              \
+    if (a.split_ok) hipLaunchKernelGGL((prefill_pp<T, D, true>), g, block, 0, s, a);                \
+    else hipLaunchKernelGGL((prefill_pp<T, D, false>), g, block, 0, s, a);                          \
+  } while (0)
+    if (dtype == LI_BF16) {
+      if (a.head_dim == 128) LI_PP(li_bf16, 128);
+      else LI_PP(li_bf16, 64);
+    } else {
+      if (a.head_dim == 128) LI_PP(li_f16, 128);
+      else LI_PP(li_f16, 64);
+    }
+#undef LI_PP
   }
-  return check_launch("prefill_mfma");
+  if (int rc = check_launch("prefill_mfma")) return rc;
+  return launch_prefill_merge(a, dtype, s);
+}
+
+// After a pass that may be split: one work-group per (work-list entry that
+// can hold a piece, KV head); those of a split block's first piece fold it.
+static int launch_prefill_merge(const AttnArgs& a, int dtype, hipStream_t s) {
+  if (!a.split_ok) return LI_OK;
+  const int chunks = kMinRows / (a.head_dim == 128 ? merge_rows<128>() : merge_rows<64>());
+  const dim3 g((unsigned)(prefill_split_blocks_cap(a.split_target, a.num_kv_heads) * a.num_kv_heads * chunks)),
+      block(256);
+  if (dtype == LI_BF16) {
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_merge<li_bf16, 128>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_merge<li_bf16, 64>), g, block, 0, s, a);
+  } else {
+    if (a.head_dim == 128) hipLaunchKernelGGL((prefill_merge<li_f16, 128>), g, block, 0, s, a);
+    else hipLaunchKernelGGL((prefill_merge<li_f16, 64>), g, block, 0, s, a);
+  }
+  return check_launch("prefill_merge");
 }
 
 int launch_prefill_mfma(const AttnArgs& in, int dtype, hipStream_t s) {

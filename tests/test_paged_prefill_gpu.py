@@ -51,6 +51,27 @@ def test_long_rows_beside_a_chunk_cut_into_many_pieces(dtype):
     assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
 
 
+@pytest.mark.parametrize(
+    ("contexts", "query_lens", "dtype", "head_dim", "num_heads", "num_kv_heads"),
+    [
+        ([4160], [64], torch.bfloat16, 128, 32, 8),  # one block over a long prefix: cut into pieces
+        ([15512], [512], torch.bfloat16, 64, 32, 8),  # eight blocks, each cut
+        ([2100, 9000], [100, 37], torch.float16, 128, 32, 8),  # two sequences, partial blocks
+        ([6000], [300], torch.bfloat16, 128, 16, 2),  # two KV heads: one queue, eight groups
+        ([700, 5000, 90], [700, 64, 1], torch.bfloat16, 128, 32, 8),  # a one-query row keeps the pass whole
+        ([200], [150], torch.bfloat16, 128, 32, 8),  # too short to cut
+    ],
+    ids=["64-over-4096", "512-over-15000", "two-f16", "two-kv-heads", "with-a-row", "short"],
+)
+def test_a_small_pass_cut_into_pieces(contexts, query_lens, dtype, head_dim, num_heads, num_kv_heads):
+    """A pass whose blocks would leave most of the grid idle has each
+    block's fully visible key stages cut into pieces folded by different
+    work-groups and merged after the launch: same answer as the oracle."""
+    b = PagedBatch(contexts, query_lens, dtype=dtype, num_heads=num_heads, num_kv_heads=num_kv_heads,
+                   head_dim=head_dim, num_slots=1 << 15, seed=len(contexts) + head_dim)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+
+
 @pytest.mark.parametrize("block_q", [1, 4, 16, 32])
 def test_the_answer_does_not_depend_on_the_query_block(block_q):
     b = PagedBatch([100, 16, 47, 9], [33, 16, 15, 1], num_slots=2048)
