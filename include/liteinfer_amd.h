@@ -308,8 +308,12 @@ int li_paged_decode_noalloc(const void* q, int64_t q_stride_seq,
  * a slot table `max_context` wide on a device of `num_cus` compute units
  * (0 = ask the current device): partials of its one-query sequences, which
  * the decode kernel's balanced split serves with a partitioned key axis (run
- * by the first work-groups of the prefill launch), and the list that orders
- * the prefill kernel's query blocks longest first. No counterpart in
+ * by the first work-groups of the prefill launch), the list that orders
+ * the prefill kernel's query blocks longest first, and -- when batch x
+ * num_kv_heads x 2 does not exceed the prefill grid (small batches) -- room
+ * for the partial rows of a pass whose blocks are cut into pieces (one
+ * 256-row fp32 slot per unit of the grid, ~34 MB at head_dim 128 on 256
+ * CUs). No counterpart in
  * the reference, whose prefill kernel allocates nothing
  * (liteinfer/models/paged_kernels.py:867). The size is for the current
  * device (its CU count sizes the grid the launch runs); num_cus is accepted
