@@ -162,6 +162,58 @@ def test_captured_packed_pass_with_rows_matches_eager_on_every_replay():
         assert np.isfinite(replayed.float().cpu().numpy()).all()
 
 
+def test_captured_small_pass_cut_into_pieces_matches_eager_on_every_replay():
+    """A pass small enough to be cut into pieces (two sequences of at most
+    64 queries over up to 8,192 keys), captured once: the pieces are chosen
+    on the device on every replay from the lengths it finds, and the merge
+    after the launch folds however many there are (none when a one-query
+    row keeps the pass whole)."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    g = torch.Generator(device=DEV).manual_seed(9)
+    batch, width, heads, kv_heads, dim, num_slots = 2, 8192, 32, 8, 128, 1 << 15
+    bf = torch.bfloat16
+    key_pool = torch.randn(num_slots, kv_heads, dim, generator=g, device=DEV).to(bf)
+    value_pool = torch.randn(num_slots, kv_heads, dim, generator=g, device=DEV).to(bf)
+    query = torch.empty(128, heads, dim, dtype=bf, device=DEV)
+    slot_table = torch.empty(batch, width, dtype=torch.int64, device=DEV)
+    context_lens = torch.empty(batch, dtype=torch.int32, device=DEV)
+    qsl = torch.empty(batch + 1, dtype=torch.int32, device=DEV)
+    max_query_len = 64
+
+    def refill(qlens, ctx, seed):
+        gg = torch.Generator(device=DEV).manual_seed(seed)
+        context_lens.copy_(torch.tensor(ctx, dtype=torch.int32))
+        qsl.copy_(torch.tensor([0, *np.cumsum(qlens).tolist()], dtype=torch.int32))
+        slot_table.copy_(torch.randint(0, num_slots, (batch, width), generator=gg, device=DEV))
+        query.copy_(torch.randn(query.shape, generator=gg, device=DEV).to(bf))
+
+    def run():
+        return paged_prefill(query, key_pool, value_pool, slot_table, context_lens, qsl, max_query_len,
+                             dim ** -0.5, heads // kv_heads)
+
+    refill([64, 64], [8192, 3000], 0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+    cases = (([64, 64], [8192, 3000]), ([10, 50], [600, 7000]), ([64, 1], [5000, 4000]),
+             ([33, 64], [64, 8192]), ([64, 64], [2048, 2048]))
+    for i, (qlens, ctx) in enumerate(cases):
+        refill(qlens, ctx, 20 + i)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out[:sum(qlens)].clone()
+        eager = run()[:sum(qlens)]
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), (qlens, ctx)
+        assert np.isfinite(replayed.float().cpu().numpy()).all()
+
+
 def test_plain_capture_after_an_engine_capture():
     """An engine that captured its decode graphs leaves no state that breaks a later capture.
 
