@@ -595,6 +595,8 @@ def main() -> int:
                         help="time only this packed prefill pass (for profiling) and print its line")
     parser.add_argument("--only-step", action="store_true",
                         help="time only config 2's fused decode step (for profiling) and print its line")
+    parser.add_argument("--no-reference-shapes", action="store_true",
+                        help="skip the reference's own benchmark shapes (Llama-3.2-1B geometry)")
     parser.add_argument("--only-reference-shapes", action="store_true",
                         help="time only the reference's own benchmark shapes (Llama-3.2-1B geometry) and print them")
     args = parser.parse_args()
@@ -795,7 +797,8 @@ def main() -> int:
         torch.cuda.empty_cache()
         secondary["rope_kv_write_c3"] = _time_rope(1, c3_tokens, geo3)
         secondary["rope_kv_write_c2"] = _time_rope(64, 1, geo3)
-        secondary["reference_a40_shapes"] = _reference_shapes(args.seed)
+        if not args.no_reference_shapes:
+            secondary["reference_a40_shapes"] = _reference_shapes(args.seed)
         result["secondary"] = secondary
         torch.cuda.empty_cache()
         step = None
