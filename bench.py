@@ -51,6 +51,7 @@ from liteinfer_amd import _native  # noqa: E402
 from liteinfer_amd.attention import PagedKV, paged_attention  # noqa: E402
 from liteinfer_amd.cache.kv_cache import scatter_into  # noqa: E402
 from liteinfer_amd.paged_kernels import kv_scatter, paged_decode  # noqa: E402
+from liteinfer_amd.engine.runner import graph_capture  # noqa: E402
 from liteinfer_amd.workloads import LLAMA_3_2_1B, c3_shapes, decode_step, packed_step  # noqa: E402
 
 METRIC = "paged-decode HBM GB/s (% of peak); prefill attn TFLOP/s; e2e output tok/s"
@@ -157,7 +158,7 @@ def _time_step(step, steps, warmup):
         one()
     stream.wait_stream(side)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with graph_capture(graph):
         one()
     for _ in range(warmup):
         graph.replay()
@@ -216,7 +217,7 @@ def graph_replay_us(fn, replays: int = 100, repeats: int = 5, calls: int = 1) ->
             fn()
     torch.cuda.current_stream().wait_stream(side)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with graph_capture(graph):
         for _ in range(calls):
             fn()
     graph.replay()
@@ -310,7 +311,7 @@ def _time_rope(batch, tokens, geo, iters=50, num_slots=1 << 20, seed=0):
                 fn()
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with graph_capture(graph):
             for _ in range(calls):
                 fn()
         graph.replay()

@@ -20,6 +20,7 @@ from __future__ import annotations
 from collections.abc import Sequence
 from typing import NamedTuple
 
+import numpy as np
 import torch
 
 
@@ -126,10 +127,13 @@ def _block_matrix(
     whole batch crosses to the device in a single transfer (block_pool.py:103-121).
     """
     width = max(len(table) for table in block_tables)
-    rows = []
+    lead = len(leading)
+    matrix = np.zeros((len(block_tables), lead + width), dtype=np.int64)
+    for j, column in enumerate(leading):
+        matrix[:, j] = column
     for i, table in enumerate(block_tables):
-        rows.append([column[i] for column in leading] + list(table) + [0] * (width - len(table)))
-    return torch.tensor(rows, dtype=torch.long, device=device)
+        matrix[i, lead:lead + len(table)] = table
+    return torch.from_numpy(matrix).to(device)
 
 
 def _position_slots(blocks: torch.Tensor, width: int, block_size: int) -> torch.Tensor:

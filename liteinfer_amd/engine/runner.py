@@ -11,6 +11,8 @@ Every address is built before the forward, so the forward holds no host work.
 
 from __future__ import annotations
 
+import contextlib
+import gc
 from dataclasses import dataclass
 
 import torch
@@ -30,6 +32,24 @@ class _Chunk:
     @property
     def end(self) -> int:
         return self.start + len(self.token_ids)
+
+
+@contextlib.contextmanager
+def graph_capture(graph: torch.cuda.CUDAGraph, pool=None):
+    """`torch.cuda.graph(graph, pool)` with Python's cyclic garbage collector off
+    for the capture: a collection inside it would run the destructors of
+    whatever unreachable cycles hold (device tensors, graphs) while the stream
+    captures, and such a collection inside a captured decode forward has
+    aborted the process. (torch collects once just before the capture
+    begins; the collector is on again after it.)"""
+    was_enabled = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph, pool=pool):
+            yield
+    finally:
+        if was_enabled:
+            gc.enable()
 
 
 class DecodeGraphs:
@@ -84,7 +104,7 @@ class DecodeGraphs:
         graph = torch.cuda.CUDAGraph()
         if self._pool is None:
             self._pool = torch.cuda.graph_pool_handle()
-        with torch.cuda.graph(graph, pool=self._pool):
+        with graph_capture(graph, pool=self._pool):
             out = self._forward(width)
         self._graphs[width] = (graph, out)
         self.captured_widths.append(width)
