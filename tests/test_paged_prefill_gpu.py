@@ -60,8 +60,12 @@ def test_long_rows_beside_a_chunk_cut_into_many_pieces(dtype):
         ([6000], [300], torch.bfloat16, 128, 16, 2),  # two KV heads: one queue, eight groups
         ([700, 5000, 90], [700, 64, 1], torch.bfloat16, 128, 32, 8),  # a one-query row keeps the pass whole
         ([200], [150], torch.bfloat16, 128, 32, 8),  # too short to cut
+        ([5032], [32], torch.bfloat16, 128, 64, 4),  # 16 heads per KV head: 16-query blocks
+        ([3300, 2100], [300, 5], torch.bfloat16, 128, 8, 8),  # one head per KV head: 256-query blocks
+        ([1100 + 37 * i for i in range(16)], [20 + i for i in range(16)], torch.float16, 64, 32, 8),  # 16 sequences
     ],
-    ids=["64-over-4096", "512-over-15000", "two-f16", "two-kv-heads", "with-a-row", "short"],
+    ids=["64-over-4096", "512-over-15000", "two-f16", "two-kv-heads", "with-a-row", "short", "g16", "g1",
+         "sixteen"],
 )
 def test_a_small_pass_cut_into_pieces(contexts, query_lens, dtype, head_dim, num_heads, num_kv_heads):
     """A pass whose blocks would leave most of the grid idle has each
