@@ -24,9 +24,11 @@ over an fp8 (e4m3) KV pool, and so is the fused RoPE + slot-write at config 3's
 packed pass and config 2's decode step, with the reference's separate torch
 ops timed on the same inputs, and config 5: `LLM.generate` of 256 requests x
 256 greedy tokens over a random-initialised Llama-3-8B-architecture model
-(output tokens per second, liteinfer_amd/engine/e2e.py). `cpu_baseline` times the dense eager attention
-(oracle/baseline.py) in fp32 on this host's cores over a bounded sample of the
-same step.
+(output tokens per second, liteinfer_amd/engine/e2e.py). `reference_a40_shapes`
+times this build's calls on the shapes of the reference's own published
+benchmark tables (Llama-3.2-1B geometry), beside its A40 figures.
+`cpu_baseline` times the dense eager attention (oracle/baseline.py) in fp32 on
+this host's cores over a bounded sample of the same step.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
