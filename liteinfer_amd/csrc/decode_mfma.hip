@@ -184,8 +184,8 @@ __global__ __launch_bounds__(64 * P) void decode_grouped(AttnArgs a) {
       const int take = min(32 * t_hi, ctx) - key0;
       const int h0 = (grp * P + pw) * HG;  // the group's first KV head
       if (t_lo == 0 && lane < HG) {
-        // This wave holds the context's first key: the waves holding its
-        // pieces, for each head of the group.
+        // This wave holds the context's first key: the work-groups holding
+        // its pieces, for each head of the group.
         const int64_t seg = (int64_t)grp * per_group + before;
         a.pieces[(int64_t)seq * a.num_kv_heads + h0 + lane] =
             int4{w, (int)((seg + nu - 1) / share), first_segment ? 0 : 1, 0};

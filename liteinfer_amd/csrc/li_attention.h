@@ -40,7 +40,7 @@ struct AttnArgs {
   int max_query_len;      // most queries any sequence brings (prefill)
   int max_context;        // slot-table width (prefill)
   int single_query_elsewhere;  // prefill: one-query sequences are served by the decode kernel
-  int4* pieces;  // balanced decode: per (sequence, KV head) {first wave, last wave, first slot}
+  int4* pieces;  // balanced decode: per (sequence, KV head) {first work-group, last work-group, first slot}
   int part_heads;  // balanced decode: KV heads per partial slot (1; kDecodeHeadGroup when head-grouped)
   int seg_cost;    // head-grouped decode: work units charged per segment start, on top of its 32-key tiles
   int4* work;    // MFMA prefill: query blocks, heaviest first, each {sequence * num_qblocks + block, the
