@@ -523,6 +523,104 @@ __global__ __launch_bounds__(64 * NW) void combine_wide(AttnArgs a) {
   *reinterpret_cast<uint32_t*>(orow + d0) = li_pack2<T>(o.x * inv, o.y * inv);
 }
 
+// ---------------------------------------------------------------------------
+// Short decode: one work-group of NW waves per (sequence, KV head), for
+// launches whose every context is short (the slot table's width bounds them).
+// Wave v folds the v-th of NW equal, tile-aligned runs of the context; the
+// waves then merge their softmax states through LDS (each state's rows
+// weighted by 2^(m_v - max m), as the reference's cross-partition reduce
+// weights its partitions, liteinfer/models/paged_kernels.py:574-629) and
+// write the normalised rows. One launch, no partial rows in HBM and no
+// combine launch: a call is its loads' round trips and one launch. Over a
+// 16-bit pool it also writes the step's newest K / V rows (a.new_k).
+// ---------------------------------------------------------------------------
+template <typename T, int D, bool F8, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_short(AttnArgs a) {
+  using Lds = DecodeLds<D, F8, kShortChunk>;
+  static_assert(sizeof(Lds::stage) >= 16 * D * sizeof(float), "a wave's state fits its stages");
+  __shared__ __attribute__((aligned(1024))) Lds lds_of[NW];
+  __shared__ float s_m[NW][16], s_l[NW][16];
+  const int lane = threadIdx.x & 63, wv = (int)(threadIdx.x >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int seq = blockIdx.x / a.num_kv_heads, kvh = blockIdx.x % a.num_kv_heads;
+  const int G = a.groups;
+  const int keys = decode_keys(a, seq);
+  const int row = decode_row(a, seq);
+  if (row < 0) return;
+  // Wave wv's run: [wv * per, (wv + 1) * per) of the context, whole tiles.
+  const int per = ((keys + NW - 1) / NW + 31) / 32 * 32;
+  const int kb = min(wv * per, keys), ke = min(kb + per, keys);
+  if constexpr (!F8) {
+    if (a.new_k != nullptr && kb < ke && ke == keys) {
+      // This wave folds the context's last key: the step's new K and V rows
+      // of this KV head go to that key's slot first (lane (kv, c) stores
+      // 16-byte chunk c of K or V), and the wave waits for the stores before
+      // its loads read the slot back. No other work-group reads these bytes
+      // (other KV heads' rows, other sequences' slots).
+      constexpr int kCh = D / 8;
+      const int64_t slot = a.st[(int64_t)seq * a.st_s + keys - 1];
+      if (lane < 2 * kCh) {
+        const int kv = lane / kCh, c = lane % kCh;
+        if (slot >= 0 && slot < a.num_slots) {
+          const T* src = static_cast<const T*>(kv ? a.new_v : a.new_k) + (int64_t)seq * a.n_s0 +
+                         (int64_t)kvh * a.n_s1 + 8 * c;
+          char* dst = static_cast<char*>(const_cast<void*>(kv ? a.vp : a.kp)) +
+                      (slot * a.p_s0 + (int64_t)kvh * a.p_s1) * (int64_t)sizeof(T) + 16 * c;
+          *reinterpret_cast<u32x4_t*>(dst) = *reinterpret_cast<const u32x4_t*>(src);
+        } else if (lane == 0 && kvh == 0 && a.bad) {
+          atomicAdd(a.bad, 1);  // once per sequence, as the slot-write counts
+        }
+      }
+      li_wait_vm<0>();
+    }
+  }
+  DecodeState st;
+  reset_state(st);
+  if (ke > kb) {
+    DecodeQuery<T, D, F8> q;
+    load_query(a, row, kvh, q);
+    fold_keys<T, D, F8>(a, lds_of[wv], q, seq, kvh, kb, ke, st);
+  }
+  // Each wave's state into its own stages (its loads have drained): head n's
+  // accumulator row, its running maximum and its denominator.
+  const float lt = li_group_sum(st.l);
+  float* acc = reinterpret_cast<float*>(lds_of[wv].stage);
+  if (n < G) {
+#pragma unroll
+    for (int blk = 0; blk < D / 16; ++blk)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[n * D + 16 * blk + 4 * g + r] = st.acc[blk][r];
+    if (g == 0) {
+      s_m[wv][n] = st.m;
+      s_l[wv][n] = lt;
+    }
+  }
+  __syncthreads();
+  const float vscale = F8 ? a.v_scale : 1.f;
+  T* orow = static_cast<T*>(a.out) + (int64_t)row * a.o_s0 + (int64_t)kvh * G * a.o_s1;
+  for (int e = threadIdx.x; e < G * D; e += 64 * NW) {
+    const int h = e / D, d = e % D;
+    if (keys == 0) {  // no key to attend to: the reference's softmax over nothing is 0 / 0
+      orow[(int64_t)h * a.o_s1 + d] = li_quiet_nan<T>();
+      continue;
+    }
+    {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) mx = fmaxf(mx, s_m[v][h]);
+      float num = 0.f, den = 0.f;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) {
+        // A wave with no keys holds m = -inf, l = 0 and zero rows.
+        const float wgt = s_l[v][h] > 0.f ? __builtin_amdgcn_exp2f(s_m[v][h] - mx) : 0.f;
+        num = fmaf(wgt, reinterpret_cast<const float*>(lds_of[v].stage)[h * D + d], num);
+        den = fmaf(wgt, s_l[v][h], den);
+      }
+      orow[(int64_t)h * a.o_s1 + d] = li_from_float<T>(num * (vscale / den));
+    }
+  }
+}
+
 bool rows_aligned(const void* p, int64_t s0, int64_t s1, int esize) {
   return aligned16(p) && (s0 * esize) % 16 == 0 && (s1 * esize) % 16 == 0;
 }
@@ -569,6 +667,38 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s) {
 #undef LI_DECODE_LAUNCH
   if (int rc = check_launch("decode_mfma")) return rc;
   return balanced ? launch_combine_balanced(a, dtype, s) : LI_OK;
+}
+
+bool decode_short_applies(const AttnArgs& a, int dtype, int max_context) {
+  if (a.qsl || !decode_mfma_applies(a, dtype)) return false;
+  const int64_t segments = (int64_t)a.batch * a.num_kv_heads;
+  // Measured against the balanced split (uniform contexts at 32 / 8 heads,
+  // head_dim 64 and 128, 1 to 128 sequences, one graph of 20 calls): the
+  // short kernel wins while its work-groups fit about two rounds of the chip
+  // (segments x width up to 2^19 keys) and no wave folds more than about
+  // 256 keys (width up to 1024; up to 2048 once there are 128 segments, so
+  // that a wave's run stays short).
+  if (segments * max_context > kShortMaxKeySegments) return false;
+  return max_context <= kShortMaxWidth || (max_context <= 2 * kShortMaxWidth && segments >= kShortWideSegments);
+}
+
+int launch_decode_short(const AttnArgs& a, int dtype, hipStream_t s) {
+  const int64_t blocks = (int64_t)a.batch * a.num_kv_heads;
+  if (blocks == 0) return LI_OK;
+  if (blocks > 0x7fffffffLL) return fail(LI_EUNSUPPORTED, "decode grid of %lld blocks is too large", (long long)blocks);
+  const dim3 grid((unsigned)blocks);
+  // Waves per work-group: as many as the LDS holds (two tile stages each).
+  if (a.kv_fp8) {
+    if (dtype == LI_BF16) hipLaunchKernelGGL((decode_short<li_bf16, 128, true, 8>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((decode_short<li_f16, 128, true, 8>), grid, dim3(512), 0, s, a);
+  } else if (dtype == LI_BF16) {
+    if (a.head_dim == 128) hipLaunchKernelGGL((decode_short<li_bf16, 128, false, 4>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((decode_short<li_bf16, 64, false, 8>), grid, dim3(512), 0, s, a);
+  } else {
+    if (a.head_dim == 128) hipLaunchKernelGGL((decode_short<li_f16, 128, false, 4>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((decode_short<li_f16, 64, false, 8>), grid, dim3(512), 0, s, a);
+  }
+  return check_launch("decode_short");
 }
 
 int launch_combine_balanced(const AttnArgs& a, int dtype, hipStream_t s) {

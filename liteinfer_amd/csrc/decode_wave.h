@@ -90,10 +90,11 @@ __device__ __forceinline__ void issue_tile(char* stage, const char* __restrict__
   }
 }
 
-// LDS of one decode wave: the staged slots of a chunk and two tile stages.
-template <int D, bool F8>
+// LDS of one decode wave: the staged slots of a chunk of kChunk keys (a
+// multiple of 64) and two tile stages.
+template <int D, bool F8, int kChunk = kSlotChunk>
 struct DecodeLds {
-  int sl[kSlotChunk + 64];
+  int sl[kChunk + 64];
   char stage[2][KvTile<D, F8>::kTileBytes];
 };
 
@@ -294,9 +295,10 @@ __device__ __forceinline__ void fold_tile(uint32_t stage, int t0, int te, const 
 }
 
 // Folds keys [kb, ke) of sequence `seq`'s context for KV head `kvh` into `st`.
-template <typename T, int D, bool F8>
-__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& lds, const DecodeQuery<T, D, F8>& q,
-                                          int seq, int kvh, int kb, int ke, DecodeState& st) {
+template <typename T, int D, bool F8, int kChunk>
+__device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8, kChunk>& lds,
+                                          const DecodeQuery<T, D, F8>& q, int seq, int kvh, int kb, int ke,
+                                          DecodeState& st) {
   using L = KvTile<D, F8>;
   const int lane = li_lane();
   const TileOffsets<D, F8> off;
@@ -308,19 +310,19 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& l
   // An fp8 pool stores K / k_scale: its scale multiplies the scores.
   const float sc = a.scale * (F8 ? a.k_scale * q.scale : 1.f) * kLog2eMfma;
 
-  for (int c0 = kb; c0 < ke; c0 += kSlotChunk) {
-    const int c1 = min(c0 + kSlotChunk, ke);
+  for (int c0 = kb; c0 < ke; c0 += kChunk) {
+    const int c1 = min(c0 + kChunk, ke);
     const int ntiles = (c1 - c0 + 31) / 32;
     // Stage this chunk's slots (int32: a pool holds fewer than 2^31 slots),
     // plus a tile past its end. Entries past the chunk repeat its last slot,
     // so the loads of a partial or look-ahead tile read real rows; their
     // scores are masked.
     {
-      int vals[kSlotChunk / 64 + 1];
+      int vals[kChunk / 64 + 1];
 #pragma unroll
-      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
+      for (int k = 0; k < kChunk / 64 + 1; ++k) vals[k] = (int)srow[min(c0 + lane + 64 * k, c1 - 1)];
 #pragma unroll
-      for (int k = 0; k < kSlotChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
+      for (int k = 0; k < kChunk / 64 + 1; ++k) lds.sl[lane + 64 * k] = vals[k];
     }
 
     auto fold = [&](uint32_t stage, int t0) __attribute__((always_inline)) {
@@ -334,11 +336,11 @@ __device__ __forceinline__ void fold_keys(const AttnArgs& a, DecodeLds<D, F8>& l
     constexpr int kInFlight = 2 * L::kInsts;
     issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, 0, lane);
     for (int ti = 0;;) {
-      issue_tile<D, F8>(lds.stage[1], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kSlotChunk), lane);
+      issue_tile<D, F8>(lds.stage[1], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kChunk), lane);
       li_wait_vm<kInFlight>();
       fold(lds_addr(lds.stage[0]), c0 + 32 * ti);
       if (++ti >= ntiles) break;
-      issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kSlotChunk), lane);
+      issue_tile<D, F8>(lds.stage[0], kpool, vpool, lds.sl, row_bytes, min(32 * (ti + 1), kChunk), lane);
       li_wait_vm<kInFlight>();
       fold(lds_addr(lds.stage[1]), c0 + 32 * ti);
       if (++ti >= ntiles) break;

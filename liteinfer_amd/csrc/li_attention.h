@@ -179,6 +179,21 @@ int launch_combine(const AttnArgs& a, int dtype, hipStream_t s);
 bool decode_mfma_applies(const AttnArgs& a, int dtype);
 int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s);
 
+// Short decode (decode_short, decode_mfma.hip): one work-group per
+// (sequence, KV head) whose waves split the context and merge their states
+// in LDS, for launches whose contexts are all short (max_context, the slot
+// table's width, bounds them): one launch, no partial rows, no combine.
+// kShortChunk is the slots a wave stages at a time.
+constexpr int kShortChunk = 256;
+// Its rule: segments (sequence, KV head) x max_context at most
+// kShortMaxKeySegments, and max_context at most kShortMaxWidth, or twice that
+// with at least kShortWideSegments segments.
+constexpr long long kShortMaxKeySegments = 1 << 19;
+constexpr int kShortMaxWidth = 1024;
+constexpr int kShortWideSegments = 128;
+bool decode_short_applies(const AttnArgs& a, int dtype, int max_context);
+int launch_decode_short(const AttnArgs& a, int dtype, hipStream_t s);
+
 // MFMA prefill: same applicability rules as decode.
 bool prefill_mfma_applies(const AttnArgs& a, int dtype);
 int launch_prefill_mfma(const AttnArgs& a, int dtype, hipStream_t s);

@@ -296,14 +296,17 @@ int paged_decode_impl(const void* q, int64_t q_stride_seq, int64_t q_stride_head
     return fail(LI_EUNSUPPORTED,
                 "li_paged_decode: fp8 pools run on the MFMA kernel only (bf16 / fp16 queries, head_dim 128, "
                 "16-byte aligned rows)");
-  const bool balanced = mfma && (num_splits == 0 || !(flags & LI_FLAG_EQUAL_SPLITS));
+  // Every context short (the table's width bounds them): one work-group per
+  // (sequence, KV head), one launch. A pinned split count keeps its kernel.
+  const bool short_call = mfma && !(flags & LI_FLAG_EQUAL_SPLITS) && decode_short_applies(a, dtype, max_context);
+  const bool balanced = !short_call && mfma && (num_splits == 0 || !(flags & LI_FLAG_EQUAL_SPLITS));
   const bool grouped = balanced && balanced_part_heads(num_kv_heads) % kDecodeHeadGroup == 0;
   if (newest && newest->k) {
-    // The head-grouped kernel over a 16-bit pool writes the newest rows
-    // itself (16-byte aligned rows); anywhere else a write of them runs
-    // first, into the slots the table names.
+    // The head-grouped and short kernels over a 16-bit pool write the newest
+    // rows themselves (16-byte aligned rows); anywhere else a write of them
+    // runs first, into the slots the table names.
     const int esize = dtype_size(dtype);
-    const bool fused = grouped && !a.kv_fp8 && aligned16(newest->k) && aligned16(newest->v) &&
+    const bool fused = (grouped || short_call) && !a.kv_fp8 && aligned16(newest->k) && aligned16(newest->v) &&
                        (newest->s0 * esize) % 16 == 0 && (newest->s1 * esize) % 16 == 0;
     if (fused) {
       a.new_k = newest->k;
@@ -330,6 +333,7 @@ int paged_decode_impl(const void* q, int64_t q_stride_seq, int64_t q_stride_head
       clear_error();
     }
   }
+  if (short_call) return launch_decode_short(a, dtype, s);
   if (balanced) {
     // The MFMA kernel's schedule: the balanced split (it launches its own
     // combine). A split count the caller chose (the engine passes

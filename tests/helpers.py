@@ -16,11 +16,13 @@ class PagedBatch:
 
     Each sequence's first context_len table columns are random slots in
     [1, num_slots); the columns after them hold other random slots, which no
-    kernel may read.
+    kernel may read. The table is `width` columns wide when that is more
+    than the longest context (the width is what a decode call's kernel
+    choice sees: a wide table takes a short batch to the balanced split).
     """
 
     def __init__(self, context_lens, query_lens=None, dtype=torch.float32, num_heads=8, num_kv_heads=2,
-                 head_dim=16, num_slots=512, seed=0, device="cuda", shuffled_blocks=None):
+                 head_dim=16, num_slots=512, seed=0, device="cuda", shuffled_blocks=None, width=None):
         g = torch.Generator().manual_seed(seed)
         self.device = torch.device(device)
         self.dtype = dtype
@@ -37,7 +39,7 @@ class PagedBatch:
         self.value_pool = randn(num_slots, num_kv_heads, head_dim)
         rows = len(self.context_lens) if self.query_lens is None else sum(self.query_lens)
         self.query = randn(rows, num_heads, head_dim)
-        width = max(self.context_lens)
+        width = max(max(self.context_lens), width or 0)
         table = torch.randint(1, num_slots, (len(self.context_lens), width), generator=g, dtype=torch.int64)
         self.slot_table = table.to(self.device)
 

@@ -29,7 +29,7 @@ DEV = torch.device("cuda")
 
 class _Step:
     def __init__(self, contexts, num_heads=32, num_kv_heads=8, head_dim=128, dtype=torch.bfloat16,
-                 num_slots=1 << 15, seed=0, fill=None):
+                 num_slots=1 << 15, seed=0, fill=None, width=None):
         g = torch.Generator().manual_seed(seed)
         self.contexts = list(contexts)
         batch = len(self.contexts)
@@ -48,7 +48,7 @@ class _Step:
         self.query = randn(batch, num_heads, head_dim)
         self.new_k = randn(batch, num_kv_heads, head_dim)
         self.new_v = randn(batch, num_kv_heads, head_dim)
-        width = max(max(self.contexts), 1)
+        width = max(max(self.contexts), 1, width or 0)
         assert sum(self.contexts) + width <= num_slots
         perm = torch.randperm(num_slots, generator=g)
         table = torch.empty(batch, width, dtype=torch.int64)
@@ -94,14 +94,18 @@ def _bits(t):
     [
         ([1, 31, 32, 33, 64, 500, 4097, 8191], 32, 8, 128, torch.bfloat16),  # head-grouped, fused
         ([2000, 1, 77, 6000], 16, 8, 64, torch.float16),  # head-grouped at head_dim 64
-        ([700, 33, 1], 12, 3, 128, torch.bfloat16),  # an odd KV head count: per-head kernel, write first
+        ([700, 33, 1, 5000], 12, 3, 128, torch.bfloat16),  # an odd KV head count: per-head kernel, write first
         ([300, 5000, 12], 64, 4, 128, torch.bfloat16),  # 16 heads per KV head
         ([4000, 2, 900, 33], 32, 16, 128, torch.bfloat16),  # eight head pairs: two sets of four per work-group
+        ([1, 31, 32, 33, 64, 500], 32, 8, 128, torch.bfloat16),  # a short table: the short kernel writes them
+        ([1000, 1, 77], 16, 8, 64, torch.float16),  # short, head_dim 64
+        ([700, 33, 1], 12, 3, 128, torch.bfloat16),  # short, odd KV head count
+        ([2048] * 15 + [1], 64, 8, 128, torch.bfloat16),  # 128 segments of a 2,048-wide table: short
     ],
-    ids=["bf16-8kv", "f16-d64", "three-kv-heads", "g16", "16kv"],
+    ids=["bf16-8kv", "f16-d64", "three-kv-heads", "g16", "16kv", "short", "short-d64", "short-3kv", "short-wide"],
 )
 def test_fused_write_equals_scatter_then_decode(contexts, heads, kv_heads, dim, dtype):
-    step = _Step(contexts, heads, kv_heads, dim, dtype, seed=len(contexts))
+    step = _Step(contexts, heads, kv_heads, dim, dtype, seed=len(contexts), num_slots=1 << 16)
     (fused, kp1, vp1), (paired, kp2, vp2) = _two_ways(step)
     assert torch.equal(_bits(kp1), _bits(kp2)) and torch.equal(_bits(vp1), _bits(vp2))
     assert torch.equal(_bits(fused), _bits(paired))
@@ -142,10 +146,12 @@ def test_fused_write_matches_the_oracle():
     assert_within(out, want, 2e-2, 2e-3)
 
 
-def test_rows_past_the_newest_key_never_carry_what_the_pool_held():
+@pytest.mark.parametrize("width", [None, 4096])
+def test_rows_past_the_newest_key_never_carry_what_the_pool_held(width):
     """A pool full of NaN: the newest key's tile also stages its slot for the
-    masked keys past it, which must fold the new (finite) rows too."""
-    step = _Step([1, 5, 32, 40, 1000], seed=7, fill=float("nan"))
+    masked keys past it, which must fold the new (finite) rows too (a short
+    table: the short kernel; a wide one: the head-grouped kernel)."""
+    step = _Step([1, 5, 32, 40, 1000], seed=7, fill=float("nan"), width=width)
     kp, vp = step.pools()
     # give every context slot but the newest finite rows
     for i, c in enumerate(step.contexts):

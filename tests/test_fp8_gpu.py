@@ -68,10 +68,10 @@ def test_quantising_slot_write_is_bit_exact(src_dtype, layout, k_scale, v_scale)
 
 
 def _fp8_batch(context_lens, k_scale, v_scale, q_dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, seed=0,
-               num_slots=65536):
+               num_slots=65536, width=None):
     """A decode batch whose pools are quantised by the oracle; returns it, the fp8 pools and the fp64 oracle."""
     b = PagedBatch(context_lens, dtype=q_dtype, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=128,
-                   num_slots=num_slots, seed=seed)
+                   num_slots=num_slots, seed=seed, width=width)
     kc = fp8.quantize(to_numpy(b.key_pool), k_scale)
     vc = fp8.quantize(to_numpy(b.value_pool), v_scale)
     kd, vd = fp8.dequantize(kc, k_scale), fp8.dequantize(vc, v_scale)
@@ -97,6 +97,18 @@ def test_fp8_decode_groupings(num_heads, num_kv_heads):
                                  num_slots=8192)
     out = paged_decode(b.query, kp, vp, b.slot_table, b.context_lens_t, b.scaling, b.groups, k_scale=0.5,
                        v_scale=0.5)
+    assert_within(out, want, 2e-2, 2e-3)
+
+
+@pytest.mark.parametrize("width", [None, 4096])
+@pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (16, 1), (20, 4)])
+def test_fp8_short_contexts(num_heads, num_kv_heads, width):
+    """Contexts of at most 1,000 keys in a table as wide as the longest (the short kernel: one
+    work-group per sequence and KV head) and in a wide one (the balanced split)."""
+    b, kp, vp, want = _fp8_batch([1, 33, 300, 1000], 0.5, 0.25, num_heads=num_heads, num_kv_heads=num_kv_heads,
+                                 seed=6, num_slots=8192, width=width)
+    out = paged_decode(b.query, kp, vp, b.slot_table, b.context_lens_t, b.scaling, b.groups, k_scale=0.5,
+                       v_scale=0.25)
     assert_within(out, want, 2e-2, 2e-3)
 
 

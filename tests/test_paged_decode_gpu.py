@@ -18,6 +18,10 @@ from tests.helpers import PagedBatch, assert_within, to_numpy
 
 pytestmark = pytest.mark.gpu
 
+# A slot table this wide takes any batch to the balanced split (the short
+# kernel serves tables up to 2,048 columns).
+WIDE = 4096
+
 
 def _run(b: PagedBatch, **kw) -> torch.Tensor:
     return paged_decode(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.scaling, b.groups, **kw)
@@ -123,13 +127,15 @@ def test_bfloat16_within_rounding(kernel, num_splits):
     assert_within(_run(b, kernel=kernel, num_splits=num_splits), b.oracle(), 2 ** -6)
 
 
+@pytest.mark.parametrize("width", [None, WIDE])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize(("num_heads", "num_kv_heads"), [(32, 8), (8, 8), (10, 2), (32, 4), (16, 1)])
-def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads):
-    """Every group the MFMA kernel takes (1, 4, 5, 8, 16), contexts straddling 32-key tiles."""
+def test_mfma_kernel_shapes(dtype, head_dim, num_heads, num_kv_heads, width):
+    """Every group the MFMA kernel takes (1, 4, 5, 8, 16), contexts straddling 32-key tiles;
+    a table as wide as the longest context (the short kernel) and a wide one (the balanced split)."""
     b = PagedBatch([1, 31, 32, 33, 100, 257, 1000], dtype=dtype, num_heads=num_heads, num_kv_heads=num_kv_heads,
-                   head_dim=head_dim, num_slots=4096, seed=2)
+                   head_dim=head_dim, num_slots=4096, seed=2, width=width)
     want = b.oracle()
     for kernel in ("auto", "equal_splits"):
         for splits in (None, 1, 3):
@@ -148,15 +154,16 @@ def test_head_groups_sharing_work_groups(num_heads, num_kv_heads):
     assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
 
 
+@pytest.mark.parametrize("width", [None, WIDE])
 @pytest.mark.parametrize("num_kv_heads", [8, 2])
-def test_thousands_of_short_contexts(num_kv_heads):
+def test_thousands_of_short_contexts(num_kv_heads, width):
     """2,500 sequences of 1-80 keys: every work-group of the balanced grid
     walks about ten segments, and its starting sequence is found past the
     first 64 of the batch's key counts."""
     rng = np.random.default_rng(11)
     ctx = rng.integers(1, 81, size=2500).tolist()
     b = PagedBatch(ctx, dtype=torch.bfloat16, num_heads=4 * num_kv_heads, num_kv_heads=num_kv_heads,
-                   head_dim=128, num_slots=1 << 17, seed=11)
+                   head_dim=128, num_slots=1 << 17, seed=11, width=width)
     assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
 
 
@@ -202,18 +209,56 @@ def test_more_sequences_than_a_wave_has_lanes(num_heads, num_kv_heads, head_dim)
     rng = np.random.default_rng(31)
     ctx = rng.integers(1, 600, size=150).tolist()
     b = PagedBatch(ctx, dtype=torch.bfloat16, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
-                   num_slots=8192, seed=31)
+                   num_slots=8192, seed=31, width=WIDE)
     assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
 
 
+@pytest.mark.parametrize("width", [None, WIDE])
 @pytest.mark.parametrize("kernel", ["auto", "equal_splits", "generic"])
-def test_a_row_with_no_keys_is_nan_like_the_reference(kernel):
+def test_a_row_with_no_keys_is_nan_like_the_reference(kernel, width):
     """A context of 0 keys: the reference's softmax over nothing gives 0 / 0
     (NaN) for that row; the other rows are unaffected."""
     b = PagedBatch([300, 0, 45], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128, num_slots=2048,
-                   seed=9)
+                   seed=9, width=width)
     out = paged_decode(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.scaling, b.groups,
                        num_splits=2 if kernel == "equal_splits" else None, kernel=kernel)
     assert torch.isnan(out[1].float()).all()
     want = b.oracle()
     assert_within(out[[0, 2]], want[[0, 2]], 2e-2, 2e-3)
+
+
+# --- the short kernel: one work-group per (sequence, KV head) ---------------------------
+
+
+@pytest.mark.parametrize(("context_lens", "num_heads", "num_kv_heads", "head_dim", "width"), [
+    ([1], 32, 8, 64, None),                  # one key: seven of eight waves fold nothing
+    ([128], 32, 8, 64, None),                # the reference's batch-1 shape
+    ([190] * 32, 32, 8, 64, None),
+    ([1024], 32, 8, 128, None),              # the widest table at any segment count
+    ([31, 32, 33, 255, 256, 257, 1000], 16, 1, 64, None),  # runs that end inside a tile
+    ([2048] * 16, 32, 8, 64, None),          # 128 segments: a 2,048-wide table still short
+    ([700, 5, 2048] + [64] * 29, 32, 4, 128, 2048),
+    ([1024] * 64, 32, 8, 64, None),          # segments x width at the rule's limit
+    ([33, 600, 1], 64, 4, 128, None),        # 16 heads per KV head
+    ([100, 513], 10, 2, 128, None),          # a group of 5
+])
+def test_short_contexts_in_one_launch(context_lens, num_heads, num_kv_heads, head_dim, width):
+    """Batches whose table is at most 1,024 (or, over 128 segments, 2,048) columns wide run the short
+    kernel: its waves split each context into equal runs of whole tiles and merge their softmax
+    states in LDS. Runs ending inside a tile, waves with no keys, groups of 1-16, both head_dims."""
+    b = PagedBatch(context_lens, dtype=torch.bfloat16, num_heads=num_heads, num_kv_heads=num_kv_heads,
+                   head_dim=head_dim, num_slots=1 << 16, seed=41, width=width)
+    assert_within(_run(b), b.oracle(), 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_short_and_balanced_kernels_in_half_precision(head_dim):
+    """fp16 through both kernels (a tight table and a wide one), each within the bar of the oracle."""
+    b = PagedBatch([3, 77, 640, 1024], dtype=torch.float16, num_heads=32, num_kv_heads=8, head_dim=head_dim,
+                   num_slots=8192, seed=43)
+    short = _run(b)
+    wide = PagedBatch([3, 77, 640, 1024], dtype=torch.float16, num_heads=32, num_kv_heads=8, head_dim=head_dim,
+                      num_slots=8192, seed=43, width=WIDE)
+    balanced = _run(wide)
+    assert_within(short, b.oracle(), 2 ** -6, 2e-3)
+    assert_within(balanced, wide.oracle(), 2 ** -6, 2e-3)
