@@ -206,7 +206,12 @@ int li_paged_decode_plan(int batch, int num_heads, int num_kv_heads,
  * to slot_table[i, 0:context_lens[i]]. The pools hold fewer than 2^31 slots
  * (the kernels stage slot indices as 32-bit integers). fp32 accumulation;
  * the output is rounded to `dtype` once. `workspace` must hold the bytes
- * li_paged_decode_plan reports (it may be NULL when that is 0).
+ * li_paged_decode_plan reports (it may be NULL when that is 0). max_context
+ * (the table's width, which bounds every context) also picks the schedule:
+ * a narrow table (up to 1,024 columns, or 2,048 over at least 128 (sequence,
+ * KV head) pairs, with pairs x width at most 2^19) runs one work-group per
+ * (sequence, KV head) in a single launch; otherwise the balanced split and
+ * its combine. Either gives the same attention within fp32 rounding.
  */
 int li_paged_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
                     const void* key_pool, const void* value_pool,
@@ -255,10 +260,11 @@ int li_paged_decode_ex(const void* q, int64_t q_stride_seq, int64_t q_stride_hea
  *                      no write (a plain decode).
  *   num_slots, bad_slots  the pool's slot count; a newest slot outside it is
  *                      not written and is counted into *bad_slots (nullable).
- * On the balanced head-grouped MFMA kernel over a 16-bit pool the write
- * happens inside the decode launch (the wave folding a sequence's last key
- * folds the new rows from registers and stores them); elsewhere a write
- * launch runs first, with the same result. Everything else as
+ * On the balanced head-grouped and the short MFMA kernels over a 16-bit
+ * pool the write happens inside the decode launch (the wave folding a
+ * sequence's last key folds the new rows from registers and stores them, or
+ * stores them before it reads that slot); elsewhere a write launch runs
+ * first, with the same result. Everything else as
  * li_paged_decode_ex; `workspace` as li_paged_decode_plan reports.
  */
 int li_paged_decode_write(const void* q, int64_t q_stride_seq,
