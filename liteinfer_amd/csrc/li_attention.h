@@ -185,6 +185,12 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s);
 // table's width, bounds them): one launch, no partial rows, no combine.
 // kShortChunk is the slots a wave stages at a time.
 constexpr int kShortChunk = 256;
+// Sequences of a packed pass the direct prefill schedule serves (a pass
+// whose every unit has a work-group of its own, over a 16-bit pool, no
+// one-query rows in the launch, no split: no work list; work-group i takes
+// unit i / (queue count) of its queue, found by one wave's scan of the
+// sequences' query counts, and nothing after it).
+constexpr int kPrefillDirectBatch = 64;
 // Its rule: segments (sequence, KV head) x max_context at most
 // kShortMaxKeySegments, and max_context at most kShortMaxWidth, or twice that
 // with at least kShortWideSegments segments.

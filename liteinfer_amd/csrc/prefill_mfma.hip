@@ -636,7 +636,7 @@ union PpShared {
 // first work-groups fold the pass's one-query rows first (the balanced
 // decode split, AttnArgs `d`, over kRowWaves waves of each of them; their
 // count was written by prefill_order), then join the queues.
-template <typename T, int D, bool kRows, bool kSplit>
+template <typename T, int D, bool kRows, bool kSplit, bool kDirect = false>
 __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   __shared__ __attribute__((aligned(1024))) PpShared<D> lds;
   const unsigned wg = blockIdx.x;
@@ -665,7 +665,10 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   const int nqueues = a.num_kv_heads % kPrefillQueues == 0 ? kPrefillQueues : 1;
   const int qi = (int)(wg % (unsigned)nqueues);
   const int heads_per_queue = a.num_kv_heads / nqueues;
-  const int units = a.queue[kPrefillQueues] * heads_per_queue;
+  // A direct pass lists nothing: its units are found from the query counts,
+  // and every claim after a work-group's first returns kNoUnit.
+  constexpr int kNoUnit = 0x7fffffff;
+  const int units = kDirect ? kNoUnit : a.queue[kPrefillQueues] * heads_per_queue;
   // Work-group barriers here order LDS only (lds_barrier): a unit's output
   // stores and the loads in flight never hold a barrier up.
   int& s_unit = lds.pp.unit;
@@ -691,7 +694,37 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     if (e.x < 0 || e.z <= 0 || (e.z == 1 && a.single_query_elsewhere)) return false;
     return e.x % a.num_qblocks < (e.z + bq - 1) / bq;
   };
-  if (tid == 0) {
+  if constexpr (kDirect) {
+    // Unit wg / nqueues of this queue: entry (wg / nqueues) / heads_per_queue
+    // of the blocks prefill_order would list (every sequence's blocks, in
+    // sequence order), found by a scan of the sequences' block counts.
+    if (tid < 64) {
+      const int sq = lane;
+      int4 e{0, 0, 0, 0};
+      int nb = 0;
+      if (sq < a.batch) {
+        const int first = a.qsl[sq], next = a.qsl[sq + 1];
+        e = int4{first, next - first, a.ctx[sq], 0};
+        if (e.y > 0 && !(e.y == 1 && a.single_query_elsewhere)) nb = min((e.y + bq - 1) / bq, a.num_qblocks);
+      }
+      int incl = nb;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int up = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += up;
+      }
+      const int u = (int)(wg / (unsigned)nqueues);
+      const int want = u / heads_per_queue;
+      const uint64_t hit = __ballot(incl > want);
+      if (hit == 0) {
+        if (lane == 0) s_unit = kNoUnit;
+      } else if (lane == __ffsll((long long)hit) - 1) {
+        s_unit = u;
+        s_entry = int4{sq * a.num_qblocks + (want - (incl - nb)), e.x, e.y, e.z};
+        if constexpr (kSplit) s_range = int4{0, 0x7fffffff, 0, 1};
+      }
+    }
+  } else if (tid == 0) {
     const int u = atomicAdd(&a.queue[qi], 1);
     s_unit = u;
     s_entry = entry_of(u);
@@ -755,7 +788,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     // barrier at the top orders these writes before every wave's reads.
     lds_barrier();
     if (tid == 0) {
-      const int u = atomicAdd(&a.queue[qi], 1);
+      const int u = kDirect ? kNoUnit : atomicAdd(&a.queue[qi], 1);
       s_unit = u;
       s_entry = entry_of(u);
       if constexpr (kSplit) s_range = range_of(u);
@@ -1025,7 +1058,7 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
     // load, where the compiler places its wait for the atomic (this file is
     // built with the wave-level atomic optimizer off, which would otherwise
     // read the value back at once and wait for every load in flight).
-    if (j == claim_at && tid == 0) next_unit = atomicAdd(&a.queue[qi], 1);
+    if (j == claim_at && tid == 0) next_unit = kDirect ? kNoUnit : atomicAdd(&a.queue[qi], 1);
     if (!idle) {
       // The matrix phase issues ahead of the other wave's vector work on
       // its SIMD: an MFMA that waits for issue leaves the matrix core idle.
@@ -1191,9 +1224,9 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   }  // units
 }
 
-template <typename T, int D, bool kSplit>
+template <typename T, int D, bool kSplit, bool kDirect>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_pp(AttnArgs a) {
-  prefill_pp_body<T, D, false, kSplit>(a, a);
+  prefill_pp_body<T, D, false, kSplit, kDirect>(a, a);
 }
 
 // A packed pass's chunks and one-query rows in one launch: the first
@@ -1548,8 +1581,16 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
   if (rows && a.row_groups_max < 1)
     return fail(LI_EINVAL, "prefill with rows: a split of %d waves holds no work-group of %d row waves",
                 rows->num_parts, kRowWaves);
-  hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
-  if (int rc = check_launch("prefill_order")) return rc;
+  // A small pass whose every unit fits the grid at once needs no order: one
+  // work-group per unit, each finding its own, one launch.
+  const int64_t full = (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues;
+  const bool direct = !rows && !a.split_ok && !a.kv_fp8 && a.batch <= kPrefillDirectBatch && units <= full;
+  if (direct) {
+    grid = units;  // a multiple of the queue count (every KV head has a unit of each block)
+  } else {
+    hipLaunchKernelGGL(prefill_order, dim3(1), dim3(1024), 0, s, a);
+    if (int rc = check_launch("prefill_order")) return rc;
+  }
   const dim3 block(64 * W);
   const dim3 g((unsigned)grid);
   if (rows && a.kv_fp8) {
@@ -1582,8 +1623,9 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
   } else {
 #define LI_PP(T, D)                                                                                 \
   do {                                                                                              \
-    if (a.split_ok) hipLaunchKernelGGL((prefill_pp<T, D, true>), g, block, 0, s, a);                \
-    else hipLaunchKernelGGL((prefill_pp<T, D, false>), g, block, 0, s, a);                          \
+    if (a.split_ok) hipLaunchKernelGGL((prefill_pp<T, D, true, false>), g, block, 0, s, a);         \
+    else if (direct) hipLaunchKernelGGL((prefill_pp<T, D, false, true>), g, block, 0, s, a);        \
+    else hipLaunchKernelGGL((prefill_pp<T, D, false, false>), g, block, 0, s, a);                   \
   } while (0)
     if (dtype == LI_BF16) {
       if (a.head_dim == 128) LI_PP(li_bf16, 128);

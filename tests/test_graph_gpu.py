@@ -62,8 +62,11 @@ class _Step:
                             self.dim ** -0.5, self.heads // self.kv_heads)
 
 
-def test_captured_decode_step_matches_eager_on_every_replay():
-    step = _Step()
+@pytest.mark.parametrize("width", [2048, 4096])
+def test_captured_decode_step_matches_eager_on_every_replay(width):
+    """16 sequences over a 2,048-wide table run the one-launch short kernel; over a 4,096-wide
+    one, the balanced split and its combine."""
+    step = _Step(width=width)
     step.refill(0)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -251,3 +254,53 @@ def test_plain_capture_after_an_engine_capture():
     torch.cuda.synchronize()
     replayed = out.clone()
     assert torch.equal(replayed, step.run())
+
+
+def test_captured_small_pass_without_a_work_list_matches_eager_on_every_replay():
+    """A pass whose units all fit the grid at once, the caller saying it holds no one-query rows:
+    one launch, each work-group finding its unit from the query counts it reads on the device,
+    so one capture replays for any lengths within the shapes it was captured at."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    g = torch.Generator(device=DEV).manual_seed(10)
+    batch, width, heads, kv_heads, dim, num_slots = 6, 700, 32, 8, 128, 1 << 14
+    bf = torch.bfloat16
+    key_pool = torch.randn(num_slots, kv_heads, dim, generator=g, device=DEV).to(bf)
+    value_pool = torch.randn(num_slots, kv_heads, dim, generator=g, device=DEV).to(bf)
+    query = torch.empty(6 * 128, heads, dim, dtype=bf, device=DEV)
+    slot_table = torch.empty(batch, width, dtype=torch.int64, device=DEV)
+    context_lens = torch.empty(batch, dtype=torch.int32, device=DEV)
+    qsl = torch.empty(batch + 1, dtype=torch.int32, device=DEV)
+    max_query_len = 128
+
+    def refill(qlens, ctx, seed):
+        gg = torch.Generator(device=DEV).manual_seed(seed)
+        context_lens.copy_(torch.tensor(ctx, dtype=torch.int32))
+        qsl.copy_(torch.tensor([0, *np.cumsum(qlens).tolist()], dtype=torch.int32))
+        slot_table.copy_(torch.randint(0, num_slots, (batch, width), generator=gg, device=DEV))
+        query.copy_(torch.randn(query.shape, generator=gg, device=DEV).to(bf))
+
+    def run():
+        return paged_prefill(query, key_pool, value_pool, slot_table, context_lens, qsl, max_query_len,
+                             dim ** -0.5, heads // kv_heads, one_query_rows=False)
+
+    refill([128] * 6, [700] * 6, 0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = run()
+    cases = (([128] * 6, [700] * 6), ([1, 64, 65, 2, 128, 30], [1, 600, 65, 2, 700, 31]),
+             ([0, 5, 0, 128, 0, 1], [0, 5, 0, 300, 0, 9]))
+    for i, (qlens, ctx) in enumerate(cases):
+        refill(qlens, ctx, 30 + i)
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = out[:sum(qlens)].clone()
+        eager = run()[:sum(qlens)]
+        torch.cuda.synchronize()
+        assert torch.equal(replayed, eager), (qlens, ctx)
+        assert np.isfinite(replayed.float().cpu().numpy()).all()

@@ -237,3 +237,26 @@ def test_rows_and_chunks_share_the_prefill_launch(contexts, query_lens, dtype, h
     assert_within(_run(b), expected, 2 ** -6, 2e-3)
     # Folding the rows as query blocks of the prefill instead gives the same attention.
     assert_within(_run(b, one_query_rows=False), expected, 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize(("num_seqs", "num_heads", "num_kv_heads", "head_dim", "dtype", "max_q", "max_prefix"), [
+    (64, 8, 2, 128, torch.bfloat16, 60, 300),     # the most sequences the direct schedule scans
+    (32, 32, 8, 128, torch.bfloat16, 64, 3000),   # 256 units: every CU one, prefixes past 1,024 keys
+    (5, 32, 8, 64, torch.float16, 150, 90),       # several blocks a sequence, the first partial
+    (65, 8, 1, 128, torch.bfloat16, 40, 200),     # one sequence too many: the work list again
+    (3, 16, 1, 128, torch.bfloat16, 16, 0),       # 16 heads per KV head, no prefix
+])
+def test_a_small_pass_runs_one_work_group_per_unit(num_seqs, num_heads, num_kv_heads, head_dim, dtype, max_q,
+                                                   max_prefix):
+    """A pass whose (query block, KV head) units all fit the grid at once, with no one-query rows
+    in the launch, skips the work-list kernel: work-group i scans the query counts for its own
+    unit. One-query sequences are folded by the prefill kernel here (``one_query_rows=False``);
+    repeated calls agree bit for bit."""
+    rng = np.random.default_rng(num_seqs + head_dim)
+    q = rng.integers(1, max_q + 1, size=num_seqs).tolist()
+    p = rng.integers(0, max_prefix + 1, size=num_seqs).tolist()
+    b = PagedBatch([qq + pp for qq, pp in zip(q, p)], q, dtype=dtype, num_heads=num_heads,
+                   num_kv_heads=num_kv_heads, head_dim=head_dim, num_slots=1 << 17, seed=num_seqs)
+    first = _run(b, one_query_rows=False)
+    assert_within(first, b.oracle(), 2 ** -6, 2e-3)
+    assert torch.equal(_run(b, one_query_rows=False), first)
