@@ -326,7 +326,8 @@ def paged_decode(
         num_splits: how many slices each sequence's keys are cut into. On the
             MFMA kernel (bf16 / fp16) this is a scheduling hint: it runs its
             balanced split, equal keys per wave across the whole batch, for
-            any value. On the general-shape kernel, and on the MFMA kernel
+            any value (or, for a slot table narrow enough, one work-group per
+            sequence and KV head in a single launch). On the general-shape kernel, and on the MFMA kernel
             with ``kernel="equal_splits"``, an integer is the reference's rule
             (each context cut into that many equal slices) and ``None`` picks
             fixed-length partitions. The result is the same attention either
@@ -342,7 +343,8 @@ def paged_decode(
             pool at the slot of its last context position (the decode
             step's ``KVCache.scatter`` at ``newest_slots``, kv_cache.py:236-253)
             before the attention reads it: one launch where the head-grouped
-            kernel serves the shape, a write launch first elsewhere. That slot
+            or the short kernel serves the shape over a 16-bit pool, a write
+            launch first elsewhere. That slot
             must belong to no other sequence's context in the call (as every
             slot a `KVCache` hands out does).
 
