@@ -107,7 +107,10 @@ class BlockPool:
         Reads a device counter, so it waits for the writes already queued;
         call it where the caller synchronises anyway, never under capture.
         """
-        missed = int(self.bad_slots.item())
+        self.raise_if_missed(int(self.bad_slots.item()))
+
+    def raise_if_missed(self, missed: int) -> None:
+        """`check_slot_writes` on a count already read from the device counter."""
         if missed:
             self.bad_slots.zero_()
             raise IndexError(f"{missed} K/V slot writes named a slot outside the pool's "
@@ -116,6 +119,22 @@ class BlockPool:
     def slots(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
         """This layer's flat key/value stores, ``[num_slots, num_kv_heads, head_dim]``."""
         return self._keys[layer_idx], self._values[layer_idx]
+
+
+def to_device(values, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """`values` (nested lists or a numpy array) as a tensor on `device`.
+
+    To a ROCm device the host copy goes through pinned memory with an
+    asynchronous copy, so the host does not wait for the work already queued
+    on the stream (a copy from pageable memory would): an engine can stage a
+    step's addresses while the previous step still runs. torch's pinned-memory
+    cache keeps the staging buffer until the copy has read it.
+    """
+    host = torch.from_numpy(values) if isinstance(values, np.ndarray) else torch.tensor(values, dtype=dtype)
+    host = host.to(dtype)
+    if device.type != "cuda":
+        return host.to(device)
+    return host.pin_memory().to(device, non_blocking=True)
 
 
 def _block_matrix(
@@ -133,7 +152,7 @@ def _block_matrix(
         matrix[:, j] = column
     for i, table in enumerate(block_tables):
         matrix[i, lead:lead + len(table)] = table
-    return torch.from_numpy(matrix).to(device)
+    return to_device(matrix, torch.int64, device)
 
 
 def _position_slots(blocks: torch.Tensor, width: int, block_size: int) -> torch.Tensor:
@@ -163,7 +182,7 @@ def newest_slots(
     for table, position in zip(block_tables, positions, strict=True):
         block, offset = divmod(position, block_size)
         slots.append(table[block] * block_size + offset)
-    return torch.tensor([slots], dtype=torch.long, device=device)
+    return to_device([slots], torch.long, device)
 
 
 class PackedAddresses(NamedTuple):

@@ -16,12 +16,12 @@ from dataclasses import dataclass
 
 import torch
 
-from liteinfer_amd.cache.block_pool import BlockPool
+from liteinfer_amd.cache.block_pool import BlockPool, to_device
 from liteinfer_amd.cache.kv_cache import KVCache
 from liteinfer_amd.engine.model import RandomLlama
 from liteinfer_amd.engine.outputs import RequestOutput, SamplingParams
-from liteinfer_amd.engine.runner import ModelRunner
-from liteinfer_amd.engine.scheduler import Scheduler, Sequence, SequenceStatus
+from liteinfer_amd.engine.runner import ModelRunner, PendingTokens
+from liteinfer_amd.engine.scheduler import PENDING_TOKEN, Scheduler, Sequence, SequenceStatus
 from liteinfer_amd.engine.tokenizer import Tokenizer
 
 
@@ -100,33 +100,52 @@ class LLM:
             seq = Sequence(f"req-{i}", list(p), max_tokens)
             seqs.append(seq)
             self.scheduler.add(seq)
+        by_id = {s.request_id: s for s in seqs}
         steps = decode_steps = 0
         # Finiteness of every sampled logit row, kept on the device (one
         # small reduction per step, read once at the end).
         finite = torch.ones((), dtype=torch.bool, device=self.model.device)
+        # The last step's sampled tokens, still on the device: read back once
+        # the next step is launched, so the host stages step n + 1 while the
+        # GPU runs step n. Outputs end at a fixed length, so which sequences
+        # run next never depends on a token's value; the ids the next step
+        # feeds in are gathered on the device.
+        pending: PendingTokens | None = None
+        readback: tuple = ()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         try:
             while self.scheduler.has_unfinished():
                 out = self.scheduler.schedule()
                 counts = [out.num_scheduled_tokens[s.request_id] for s in out.seqs]
-                logits = self.runner.execute(out.seqs, counts)
+                logits = self.runner.execute(out.seqs, counts, pending)
+                if pending is not None:
+                    self._read_back(pending, readback, by_id)
+                    pending = None
                 steps += 1
                 decode_steps += all(c == 1 for c in counts)
                 sample = [i for i, s in enumerate(out.seqs) if s.num_computed_tokens == len(s)]
                 if sample:
-                    rows = torch.tensor(sample, device=logits.device)
-                    picked = logits.index_select(0, rows)
+                    if len(sample) == logits.shape[0]:
+                        picked = logits
+                    else:
+                        picked = logits.index_select(0, to_device(sample, torch.long, logits.device))
                     finite &= torch.isfinite(picked).all()
-                    tokens = picked.argmax(dim=-1).tolist()
-                    self.cache.pool.check_slot_writes()
-                    for i, tok in zip(sample, tokens):
+                    tokens = picked.argmax(dim=-1)
+                    index = {}
+                    for k, i in enumerate(sample):
                         seq = out.seqs[i]
-                        seq.output_token_ids.append(int(tok))
+                        seq.output_token_ids.append(PENDING_TOKEN)
+                        index[seq.request_id] = k
                         if len(seq.output_token_ids) >= seq.max_tokens:
                             seq.status = SequenceStatus.FINISHED_LENGTH
+                    pending = PendingTokens(tokens, index)
+                    readback = self._stage_read_back(tokens)
                 for seq in self.scheduler.remove_finished():
                     self.runner.release(seq)
+            if pending is not None:
+                self._read_back(pending, readback, by_id)
+                pending = None
         except BaseException:
             # A failed step (a slot write that missed the pool, a launch
             # error) leaves no sequence holding cache blocks: the LLM stays
@@ -140,3 +159,34 @@ class LLM:
         stats = GenerateStats(wall, steps, decode_steps, sum(len(p) for p in prompts),
                               sum(len(s.output_token_ids) for s in seqs), bool(finite))
         return [s.output_token_ids for s in seqs], stats
+
+    def _stage_read_back(self, tokens: torch.Tensor) -> tuple:
+        """Queue the copies of a step's sampled tokens and of the pool's missed-write counter to the host.
+
+        On a ROCm device they go into pinned memory behind the step's work,
+        with an event after them: reading them waits for that step only, not
+        for the next one, which is queued behind them by then.
+        """
+        bad = self.cache.pool.bad_slots
+        if tokens.device.type != "cuda":
+            return tokens, bad.clone(), None
+        host = torch.empty(tokens.shape, dtype=tokens.dtype, pin_memory=True)
+        host.copy_(tokens, non_blocking=True)
+        missed = torch.empty(bad.shape, dtype=bad.dtype, pin_memory=True)
+        missed.copy_(bad, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        return host, missed, done
+
+    def _read_back(self, pending: PendingTokens, readback: tuple, by_id: dict[str, Sequence]) -> None:
+        """Fill in a step's sampled tokens (waits for that step), and check the slot writes up to it."""
+        host, missed, done = readback
+        if done is not None:
+            done.synchronize()
+        tokens = host.tolist()
+        self.cache.pool.raise_if_missed(int(missed[0]))
+        for request_id, k in pending.index.items():
+            out = by_id[request_id].output_token_ids
+            if out[-1] != PENDING_TOKEN:
+                raise RuntimeError(f"{request_id}: its newest output token is not the pending one")
+            out[-1] = int(tokens[k])

@@ -17,11 +17,20 @@ from dataclasses import dataclass
 
 import torch
 
+from liteinfer_amd.cache.block_pool import to_device
 from liteinfer_amd.cache.kv_cache import KVCache
 from liteinfer_amd.engine.model import RandomLlama
-from liteinfer_amd.engine.scheduler import Sequence
+from liteinfer_amd.engine.scheduler import PENDING_TOKEN, Sequence
 
 _PAD = "__pad__"
+
+
+@dataclass
+class PendingTokens:
+    """Token ids a step sampled, still on the device: `tokens[index[request_id]]` is that sequence's."""
+
+    tokens: torch.Tensor
+    index: dict[str, int]
 
 
 @dataclass
@@ -144,8 +153,15 @@ class ModelRunner:
         self.cache.release(seq.request_id)
 
     @torch.no_grad()
-    def execute(self, seqs: list[Sequence], num_tokens: list[int]) -> torch.Tensor:
-        """One step over the next `num_tokens` of each sequence; logits at each one's last token."""
+    def execute(self, seqs: list[Sequence], num_tokens: list[int], pending: PendingTokens | None = None
+                ) -> torch.Tensor:
+        """One step over the next `num_tokens` of each sequence; logits at each one's last token.
+
+        A token id still on the device (`PENDING_TOKEN` in the sequence,
+        sampled by the step before and not read back yet) is taken from
+        `pending` on the device, so the step is staged and launched without
+        waiting for the one before it.
+        """
         ids = [s.request_id for s in seqs]
         chunks = []
         for seq, count in zip(seqs, num_tokens, strict=True):
@@ -154,29 +170,46 @@ class ModelRunner:
                 raise ValueError(f"{seq.request_id}: cannot compute {count} tokens from position {start}")
             chunks.append(_Chunk([seq.token_at(p) for p in range(start, start + count)], start))
         self.cache.reserve(ids, [c.end for c in chunks])
+        # Where a token is pending: its index in pending.tokens (-1: the id is on the host).
+        sources = [[pending.index[i] if t == PENDING_TOKEN else -1 for t in c.token_ids]
+                   for i, c in zip(ids, chunks)] if pending is not None else None
         if all(len(c.token_ids) == 1 for c in chunks):
-            logits = self._decode(ids, chunks)
+            logits = self._decode(ids, chunks, sources, pending)
         else:
-            logits = self._packed(ids, chunks)
+            logits = self._packed(ids, chunks, sources, pending)
         for seq, c in zip(seqs, chunks):
             seq.num_computed_tokens = c.end
         return logits
 
-    def _packed(self, ids: list[str], chunks: list[_Chunk]) -> torch.Tensor:
+    def _token_ids(self, host_ids: torch.Tensor, sources: torch.Tensor | None,
+                   pending: PendingTokens | None) -> torch.Tensor:
+        """The step's token ids on the device, the pending ones gathered from `pending.tokens`."""
+        if sources is None:
+            return host_ids
+        return torch.where(sources >= 0, pending.tokens[sources.clamp(min=0)], host_ids)
+
+    def _packed(self, ids: list[str], chunks: list[_Chunk], sources, pending) -> torch.Tensor:
         counts = [len(c.token_ids) for c in chunks]
         payload = self.cache.make_packed_payload(ids, [c.start for c in chunks], counts)
-        tokens = torch.tensor([[t for c in chunks for t in c.token_ids]], dtype=torch.long, device=self.device)
+        rows = [[t for c in chunks for t in c.token_ids]]
+        if sources is not None:
+            rows.append([k for per in sources for k in per])
+        staged = to_device(rows, torch.long, self.device)
+        tokens = self._token_ids(staged[0:1], staged[1:2] if sources is not None else None, pending)
         qsl = payload.addresses.query_start_loc
         return self.model.forward(tokens, payload.addresses.positions, payload, logits_positions=qsl[1:].long() - 1)
 
-    def _decode(self, ids: list[str], chunks: list[_Chunk]) -> torch.Tensor:
-        both = torch.tensor([[c.token_ids[0] for c in chunks], [c.start for c in chunks]], dtype=torch.long,
-                            device=self.device)
-        input_ids, positions = both[0].unsqueeze(1), both[1].unsqueeze(1)
+    def _decode(self, ids: list[str], chunks: list[_Chunk], sources, pending) -> torch.Tensor:
         totals = [c.end for c in chunks]
+        rows = [[c.token_ids[0] for c in chunks], [c.start for c in chunks], totals]
+        if sources is not None:
+            rows.append([per[0] for per in sources])
+        staged = to_device(rows, torch.long, self.device)
+        input_ids = self._token_ids(staged[0], staged[3] if sources is not None else None, pending).unsqueeze(1)
+        positions = staged[1].unsqueeze(1)
         write_slots = self.cache.newest_slots_for(ids, [c.start for c in chunks])
         slots = self.cache.slot_table_for(ids, totals)
-        context_lens = torch.tensor(totals, dtype=torch.int32, device=self.device)
+        context_lens = staged[2].to(torch.int32)
         if self.graphs is not None and self.graphs.has_capacity_for(len(ids)):
             return self.graphs.run(input_ids, positions, write_slots, slots, context_lens)
         payload = self.cache.make_decode_payload(write_slots, slots, context_lens, None)

@@ -16,6 +16,11 @@ from dataclasses import dataclass, field
 from enum import Enum
 
 
+# An output token sampled on the device and not read back yet (the generate
+# loop reads a step's tokens while the next step runs, and fills them in).
+PENDING_TOKEN = -1
+
+
 class SequenceStatus(str, Enum):
     WAITING = "waiting"
     RUNNING = "running"

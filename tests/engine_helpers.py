@@ -67,8 +67,8 @@ def record_logits(llm: LLM) -> list[tuple[list[str], torch.Tensor]]:
     steps: list[tuple[list[str], torch.Tensor]] = []
     execute = llm.runner.execute
 
-    def recording(seqs, num_tokens):
-        logits = execute(seqs, num_tokens)
+    def recording(seqs, num_tokens, pending=None):
+        logits = execute(seqs, num_tokens, pending)
         rows = [i for i, s in enumerate(seqs) if s.num_computed_tokens == len(s)]
         if rows:
             picked = logits.index_select(0, torch.tensor(rows, device=logits.device)).float()

@@ -85,21 +85,23 @@ def test_a_failed_step_frees_the_batch_blocks_and_the_llm_runs_again():
     llm = LLM(model, config)
     pool = llm.cache.pool
     free0 = pool.num_free_blocks
-    check = pool.check_slot_writes
+    check = pool.raise_if_missed
     calls = []
 
-    def failing():
+    def failing(missed):
+        # the loop's per-step check of the missed-write count read back with a step's tokens
         calls.append(1)
         if len(calls) == 2:
             raise IndexError("1 K/V slot writes named a slot outside the pool")
-        check()
+        check(missed)
 
-    pool.check_slot_writes = failing
+    pool.raise_if_missed = failing
     prompts = _prompts(6, 5, 70, TINY.vocab_size, seed=5)
     with pytest.raises(IndexError):
         llm.generate_ids(prompts, max_tokens=4)
+    assert len(calls) == 2
     assert pool.num_free_blocks == free0
-    pool.check_slot_writes = check
+    pool.raise_if_missed = check
     outputs, _ = llm.generate_ids(prompts, max_tokens=4)
     assert [len(o) for o in outputs] == [4] * 6
     assert pool.num_free_blocks == free0
