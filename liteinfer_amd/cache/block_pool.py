@@ -121,20 +121,42 @@ class BlockPool:
         return self._keys[layer_idx], self._values[layer_idx]
 
 
+_copy_streams: dict[int, torch.cuda.Stream] = {}
+
+
 def to_device(values, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
-    """`values` (nested lists or a numpy array) as a tensor on `device`.
+    """`values` (nested lists or a numpy array) as a tensor on `device`, ready for the current stream.
 
     To a ROCm device the host copy goes through pinned memory with an
-    asynchronous copy, so the host does not wait for the work already queued
-    on the stream (a copy from pageable memory would): an engine can stage a
-    step's addresses while the previous step still runs. torch's pinned-memory
-    cache keeps the staging buffer until the copy has read it.
+    asynchronous copy on a copy stream of its own, which the current stream
+    then waits for: the host does not wait for the work already queued (a
+    copy from pageable memory would), and the copy runs beside that work
+    instead of after it, so an engine stages a step's addresses while the
+    previous step still runs and the step starts without waiting for them.
+    torch's pinned-memory cache keeps the staging buffer until the copy has
+    read it; the result is marked as used by the current stream. (Under graph
+    capture the copy stays on the capturing stream.)
     """
     host = torch.from_numpy(values) if isinstance(values, np.ndarray) else torch.tensor(values, dtype=dtype)
     host = host.to(dtype)
     if device.type != "cuda":
         return host.to(device)
-    return host.pin_memory().to(device, non_blocking=True)
+    host = host.pin_memory()
+    if torch.cuda.is_current_stream_capturing():
+        return host.to(device, non_blocking=True)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    side = _copy_streams.get(index)
+    if side is None:
+        side = _copy_streams[index] = torch.cuda.Stream(device=index)  # default priority
+    current = torch.cuda.current_stream(index)
+    # `out` comes from the copy stream's own memory pool, whose blocks are
+    # handed out again only once every stream marked as using them is done,
+    # so the copy needs to wait for nothing the current stream has queued.
+    with torch.cuda.stream(side):
+        out = host.to(device, non_blocking=True)
+    current.wait_stream(side)
+    out.record_stream(current)
+    return out
 
 
 def _block_matrix(
