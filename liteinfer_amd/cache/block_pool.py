@@ -134,16 +134,18 @@ def to_device(values, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
     instead of after it, so an engine stages a step's addresses while the
     previous step still runs and the step starts without waiting for them.
     torch's pinned-memory cache keeps the staging buffer until the copy has
-    read it; the result is marked as used by the current stream. (Under graph
-    capture the copy stays on the capturing stream.)
+    read it; the result is marked as used by the current stream. Refused
+    inside a graph capture: a captured copy would read the staging buffer
+    again on every replay, after the cache has handed it out anew.
     """
     host = torch.from_numpy(values) if isinstance(values, np.ndarray) else torch.tensor(values, dtype=dtype)
     host = host.to(dtype)
     if device.type != "cuda":
         return host.to(device)
-    host = host.pin_memory()
     if torch.cuda.is_current_stream_capturing():
-        return host.to(device, non_blocking=True)
+        raise RuntimeError("to_device: host values cannot be staged inside a graph capture; "
+                           "copy them into the graph's static buffers before it")
+    host = host.pin_memory()
     index = device.index if device.index is not None else torch.cuda.current_device()
     side = _copy_streams.get(index)
     if side is None:
