@@ -262,3 +262,17 @@ def test_short_and_balanced_kernels_in_half_precision(head_dim):
     balanced = _run(wide)
     assert_within(short, b.oracle(), 2 ** -6, 2e-3)
     assert_within(balanced, wide.oracle(), 2 ** -6, 2e-3)
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_contexts_past_a_narrowed_tables_width_are_still_folded(head_dim):
+    """A table passed as a narrower view of a wider one (its rows keep the wider pitch), with
+    contexts past the view's width: every kernel reads slot_table[i, :ctx] through the row pitch,
+    as the reference's pointer arithmetic does, so the answer is the wide table's."""
+    b = PagedBatch([1000, 300, 700], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=head_dim,
+                   num_slots=8192, seed=47)
+    want = b.oracle()
+    narrow = b.slot_table[:, :512]
+    assert narrow.stride(0) == b.slot_table.shape[1]
+    out = paged_decode(b.query, b.key_pool, b.value_pool, narrow, b.context_lens_t, b.scaling, b.groups)
+    assert_within(out, want, 2 ** -6, 2e-3)
