@@ -172,10 +172,11 @@ def test_empty_contexts_write_nothing_and_read_nan():
     assert torch.equal(_bits(fused[[1, 3]]), _bits(paired[[1, 3]]))
 
 
-def test_fp8_pool_writes_quantised_rows_first():
+@pytest.mark.parametrize("contexts", [[300, 1, 2049], [300, 1, 900]], ids=["balanced", "short"])
+def test_fp8_pool_writes_quantised_rows_first(contexts):
     from liteinfer_amd.cache.kv_cache import quantize_fp8
 
-    step = _Step([300, 1, 2049], seed=11)
+    step = _Step(contexts, seed=11)
     ks, vs = 0.5, 0.25
     kp1 = quantize_fp8(step.key_pool, ks)
     vp1 = quantize_fp8(step.value_pool, vs)
