@@ -167,3 +167,27 @@ def test_decode_step_with_newest_rows_random_shapes(case):
     assert torch.equal(kp1.view(torch.int16), kp.view(torch.int16))
     assert torch.equal(vp1.view(torch.int16), vp.view(torch.int16))
     assert torch.equal(fused.view(torch.int16), paired.view(torch.int16))
+
+
+@pytest.mark.parametrize("case", range(10))
+def test_small_prefill_passes_without_a_work_list_random_shapes(case):
+    """Passes of at most 64 sequences, the caller saying no row is served elsewhere, sized so that
+    their (query block, KV head) units fit the grid where batch x KV heads allows (one launch,
+    each work-group finding its unit from the query counts; otherwise the listed schedule).
+    One-query sequences are folded as blocks too."""
+    rng = np.random.default_rng(9500 + case)
+    num_kv_heads = int(rng.choice([1, 2, 4, 8]))
+    groups = int(rng.choice([1, 2, 4, 8, 16]))
+    head_dim = int(rng.choice([64, 128]))
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    block_q = 256 // groups
+    batch = int(rng.integers(1, 65))
+    # keep batch x KV heads x blocks of the longest query run within the grid's 256 work-groups
+    max_blocks = max(1, 256 // (batch * num_kv_heads))
+    q = [int(rng.integers(1, block_q * max_blocks + 1)) for _ in range(batch)]
+    ctx = [qq + int(rng.integers(0, 900)) for qq in q]
+    b = PagedBatch(ctx, q, dtype=dtype, num_heads=num_kv_heads * groups, num_kv_heads=num_kv_heads,
+                   head_dim=head_dim, num_slots=1 << 16, seed=9500 + case)
+    out = paged_prefill(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.query_start_loc,
+                        max(q), b.scaling, b.groups, one_query_rows=False)
+    assert_within(out, b.oracle(), 2 ** -6, 2e-3)
