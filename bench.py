@@ -63,7 +63,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "decode_c2_traffic.json"
 # Untimed calls before each secondary workload's timed ones: enough for the
 # clocks to settle after the previous workload (a few ms of work).
 SECONDARY_WARMUP = 20
-PREFILL_WARMUP_S = 0.05
+PREFILL_WARMUP_S = 0.15
 
 
 def decode_bytes(ctxs, geo, elem=2, kv_elem=None) -> int:
@@ -182,10 +182,10 @@ def _time_prefill(step, steps, warmup):
     q = step.query.transpose(0, 1).unsqueeze(0)
     scatter_into(step.key_pool, step.value_pool, step.write_slots, step.new_k, step.new_v)
     # Warm up for `warmup` calls and at least PREFILL_WARMUP_S of them: after
-    # the memory-bound decode phases the matrix-bound prefill runs ~15% slower
-    # for its first ~30 ms (the kernel trace shows its duration falling from
-    # ~340 to ~290 us over the first ~150 config 3 calls) while the clock
-    # settles.
+    # the memory-bound decode phases the matrix-bound prefill runs up to ~15%
+    # slower for its first ~90 ms while the clock settles (a kernel trace of
+    # config 3's calls, averaged by hundreds: 330, 303, 307, 291, 289, 289,
+    # 288 us), so the figure is the sustained rate a busy server sees.
     done, t0 = 0, time.perf_counter()
     while done < warmup or time.perf_counter() - t0 < PREFILL_WARMUP_S:
         for _ in range(10):
