@@ -186,8 +186,8 @@ int launch_decode_mfma(const AttnArgs& a, int dtype, hipStream_t s);
 // kShortChunk is the slots a wave stages at a time.
 constexpr int kShortChunk = 256;
 // Sequences of a packed pass the direct prefill schedule serves (a pass
-// whose every unit has a work-group of its own, over a 16-bit pool, no
-// one-query rows in the launch, no split: no work list; work-group i takes
+// whose every unit has a work-group of its own, no one-query rows in the
+// launch, no split: no work list; work-group i takes
 // unit i / (queue count) of its queue, found by one wave's scan of the
 // sequences' query counts, and nothing after it).
 constexpr int kPrefillDirectBatch = 64;

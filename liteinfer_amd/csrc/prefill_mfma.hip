@@ -172,6 +172,33 @@ __device__ __forceinline__ void fold_rows_first(const AttnArgs& a, const AttnArg
   }
 }
 
+// The direct schedule (a pass whose every unit has a work-group of its own,
+// no work list): the block prefill_order would list at index `want` (every
+// sequence's blocks in sequence order, the same entry format), found by one
+// full wave's scan of the sequences' query counts (at most 64 sequences);
+// {-1, 0, 0, 0} past the last block. Every lane returns the entry.
+__device__ __forceinline__ int4 direct_entry(const AttnArgs& a, int want) {
+  const int lane = (int)(threadIdx.x & 63);
+  int4 e{0, 0, 0, 0};
+  int nb = 0;
+  if (lane < a.batch) {
+    const int first = a.qsl[lane], next = a.qsl[lane + 1];
+    e = int4{first, next - first, a.ctx[lane], 0};
+    if (e.y > 0 && !(e.y == 1 && a.single_query_elsewhere)) nb = min((e.y + a.block_q - 1) / a.block_q, a.num_qblocks);
+  }
+  int incl = nb;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int up = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += up;
+  }
+  const uint64_t hit = __ballot(incl > want);
+  if (hit == 0) return int4{-1, 0, 0, 0};
+  const int sq = __ffsll((long long)hit) - 1;
+  const int qb = want - (__shfl(incl, sq, 64) - __shfl(nb, sq, 64));
+  return int4{sq * a.num_qblocks + qb, __shfl(e.x, sq, 64), __shfl(e.y, sq, 64), __shfl(e.z, sq, 64)};
+}
+
 // Keys whose slots the lockstep kernel stages in LDS at a time (restaging
 // costs a pipeline drain, so chunks are long).
 constexpr int kLockstepChunk = 4096;
@@ -184,6 +211,7 @@ struct LockstepLds {
   __attribute__((aligned(1024))) char stages[2][2 * TileLayout<D>::kTileBytes];
   __attribute__((aligned(1024))) char raw[F8 ? 2 : 1][F8 ? 2 * F8Tile::kTileBytes : 16];
   int unit;
+  int4 entry;  // the direct schedule's unit
 };
 
 template <int D, bool F8>
@@ -196,7 +224,7 @@ union LockstepShared {
 // converted in LDS (convert_stage) before the fold, which is the same.
 // With kRows (prefill_mfma_rows) the first work-groups fold the pass's
 // one-query rows first (fold_rows_first).
-template <typename T, int D, int W, bool F8, bool kRows>
+template <typename T, int D, int W, bool F8, bool kRows, bool kDirect = false>
 __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d) {
   __shared__ __attribute__((aligned(1024))) LockstepShared<D, F8> lds;
   if constexpr (kRows) fold_rows_first<T, D, F8>(a, d, lds);
@@ -227,16 +255,33 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
   const int nqueues = a.num_kv_heads % kPrefillQueues == 0 ? kPrefillQueues : 1;
   const int qi = (int)(blockIdx.x % (unsigned)nqueues);
   const int heads_per_queue = a.num_kv_heads / nqueues;
-  const int units = a.queue[kPrefillQueues] * heads_per_queue;
+  // The direct schedule: work-group wg takes unit wg / nqueues of its queue
+  // (direct_entry) and nothing after it.
+  constexpr int kNoUnit = 0x7fffffff;
+  const int units = kDirect ? kNoUnit : a.queue[kPrefillQueues] * heads_per_queue;
   int& s_unit = lds.ls.unit;
+  bool claimed = false;
   for (;;) {
+  if (kDirect && claimed) break;
   __syncthreads();  // every wave is done with the previous unit's LDS
-  if (tid == 0) s_unit = atomicAdd(&a.queue[qi], 1);
+  if constexpr (kDirect) {
+    claimed = true;
+    if (w == 0) {
+      const int u = (int)(blockIdx.x / (unsigned)nqueues);
+      const int4 e = direct_entry(a, u / heads_per_queue);
+      if (lane == 0) {
+        s_unit = e.x < 0 ? kNoUnit : u;
+        lds.ls.entry = e;
+      }
+    }
+  } else if (tid == 0) {
+    s_unit = atomicAdd(&a.queue[qi], 1);
+  }
   __syncthreads();
   const int unit = s_unit;
   if (unit >= units) break;
   // The block's descriptor: one 16-byte read.
-  const int4 entry = a.work[unit / heads_per_queue];
+  const int4 entry = kDirect ? lds.ls.entry : a.work[unit / heads_per_queue];
   const int item = entry.x;
   const int seq = item / a.num_qblocks;
   const int qblock = item % a.num_qblocks;
@@ -528,9 +573,9 @@ __device__ __forceinline__ void prefill_mfma_body(AttnArgs a, const AttnArgs& d)
   }  // units
 }
 
-template <typename T, int D, int W, bool F8>
+template <typename T, int D, int W, bool F8, bool kDirect>
 __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma(AttnArgs a) {
-  prefill_mfma_body<T, D, W, F8, false>(a, a);
+  prefill_mfma_body<T, D, W, F8, false, kDirect>(a, a);
 }
 
 // A packed pass's chunks and one-query rows in one launch, fp8 pools (the
@@ -696,31 +741,13 @@ __device__ __forceinline__ void prefill_pp_body(AttnArgs a, const AttnArgs& d) {
   };
   if constexpr (kDirect) {
     // Unit wg / nqueues of this queue: entry (wg / nqueues) / heads_per_queue
-    // of the blocks prefill_order would list (every sequence's blocks, in
-    // sequence order), found by a scan of the sequences' block counts.
+    // of the blocks prefill_order would list (direct_entry).
     if (tid < 64) {
-      const int sq = lane;
-      int4 e{0, 0, 0, 0};
-      int nb = 0;
-      if (sq < a.batch) {
-        const int first = a.qsl[sq], next = a.qsl[sq + 1];
-        e = int4{first, next - first, a.ctx[sq], 0};
-        if (e.y > 0 && !(e.y == 1 && a.single_query_elsewhere)) nb = min((e.y + bq - 1) / bq, a.num_qblocks);
-      }
-      int incl = nb;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int up = __shfl_up(incl, off, 64);
-        if (lane >= off) incl += up;
-      }
       const int u = (int)(wg / (unsigned)nqueues);
-      const int want = u / heads_per_queue;
-      const uint64_t hit = __ballot(incl > want);
-      if (hit == 0) {
-        if (lane == 0) s_unit = kNoUnit;
-      } else if (lane == __ffsll((long long)hit) - 1) {
-        s_unit = u;
-        s_entry = int4{sq * a.num_qblocks + (want - (incl - nb)), e.x, e.y, e.z};
+      const int4 e = direct_entry(a, u / heads_per_queue);
+      if (lane == 0) {
+        s_unit = e.x < 0 ? kNoUnit : u;
+        s_entry = e;
         if constexpr (kSplit) s_range = int4{0, 0x7fffffff, 0, 1};
       }
     }
@@ -1584,7 +1611,7 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
   // A small pass whose every unit fits the grid at once needs no order: one
   // work-group per unit, each finding its own, one launch.
   const int64_t full = (device_cu_count() + kPrefillQueues - 1) / kPrefillQueues * kPrefillQueues;
-  const bool direct = !rows && !a.split_ok && !a.kv_fp8 && a.batch <= kPrefillDirectBatch && units <= full;
+  const bool direct = !rows && !a.split_ok && a.batch <= kPrefillDirectBatch && units <= full;
   if (direct) {
     grid = units;  // a multiple of the queue count (every KV head has a unit of each block)
   } else {
@@ -1618,8 +1645,13 @@ static int launch_prefill_waves(AttnArgs a, int dtype, hipStream_t s, const Attn
     return launch_combine_balanced(*rows, dtype, s);
   }
   if (a.kv_fp8) {
-    if (dtype == LI_BF16) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true>), g, block, 0, s, a);
-    else hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true>), g, block, 0, s, a);
+    if (dtype == LI_BF16) {
+      if (direct) hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true, true>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((prefill_mfma<li_bf16, 128, W, true, false>), g, block, 0, s, a);
+    } else {
+      if (direct) hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true, true>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((prefill_mfma<li_f16, 128, W, true, false>), g, block, 0, s, a);
+    }
   } else {
 #define LI_PP(T, D)                                                                                 \
   do {                                                                                              \

@@ -373,3 +373,24 @@ def test_quantising_slot_write_passes_nan_through(src_dtype):
         assert np.array_equal(got[~nan], want[~nan])
         assert np.all((got[nan] & 0x7F) == 0x7F)
     assert nan.sum() == 1 and ((want_k & 0x7F) == 0x7F).sum() == 2
+
+
+@pytest.mark.parametrize(("num_seqs", "num_heads", "num_kv_heads", "max_q", "max_prefix"), [
+    (64, 8, 2, 60, 300),     # the most sequences the direct schedule scans
+    (32, 32, 8, 32, 1500),   # 256 units (one block each): every CU one
+    (5, 32, 8, 100, 90),     # several blocks a sequence, the first partial
+    (65, 8, 1, 30, 200),     # one sequence too many: the work list again
+])
+def test_fp8_small_pass_without_a_work_list(num_seqs, num_heads, num_kv_heads, max_q, max_prefix):
+    """An fp8 pool's small pass with no one-query rows in the launch: the lockstep kernel's direct
+    schedule (each work-group finds its unit from the query counts; no work-list launch)."""
+    from liteinfer_amd.paged_kernels import paged_prefill
+
+    rng = np.random.default_rng(num_seqs + 3)
+    q = rng.integers(1, max_q + 1, size=num_seqs).tolist()
+    ctx = [qq + int(p) for qq, p in zip(q, rng.integers(0, max_prefix + 1, size=num_seqs))]
+    b, kp, vp, want = _fp8_packed(ctx, q, 0.5, 0.25, num_heads=num_heads, num_kv_heads=num_kv_heads,
+                                  seed=num_seqs, num_slots=1 << 17)
+    out = paged_prefill(b.query, kp, vp, b.slot_table, b.context_lens_t, b.query_start_loc, max(q), b.scaling,
+                        b.groups, k_scale=0.5, v_scale=0.25, one_query_rows=False)
+    assert_within(out, want, 2e-2, 2e-3)
