@@ -112,7 +112,7 @@ class LLM:
         # feeds in are gathered on the device.
         pending: PendingTokens | None = None
         readback: tuple = ()
-        torch.cuda.synchronize()
+        self._sync()
         t0 = time.perf_counter()
         try:
             while self.scheduler.has_unfinished():
@@ -153,12 +153,16 @@ class LLM:
             for seq in self.scheduler.abort_all():
                 self.runner.release(seq)
             raise
-        torch.cuda.synchronize()
+        self._sync()
         wall = time.perf_counter() - t0
         self.cache.pool.check_slot_writes()
         stats = GenerateStats(wall, steps, decode_steps, sum(len(p) for p in prompts),
                               sum(len(s.output_token_ids) for s in seqs), bool(finite))
         return [s.output_token_ids for s in seqs], stats
+
+    def _sync(self) -> None:
+        if self.model.device.type == "cuda":
+            torch.cuda.synchronize()
 
     def _stage_read_back(self, tokens: torch.Tensor) -> tuple:
         """Queue the copies of a step's sampled tokens and of the pool's missed-write counter to the host.
