@@ -211,6 +211,12 @@ def _paged_packed(query: torch.Tensor, kv: PagedKV, scaling: float, num_kv_group
     # pass has one-query sequences (None: the kernels find out on the device).
     one_query_rows = None
     if kv.host_query_lens:
+        if all(q == 1 for q in kv.host_query_lens):
+            # Every sequence brings one query: the pass is a decode step (token
+            # i is sequence i's query), run as one (no query offsets to read;
+            # the short kernel where the table is narrow).
+            out = _paged_decode_step(query.permute(2, 1, 0, 3), kv, scaling, num_kv_groups)  # [T, H, 1, D]
+            return out.permute(2, 1, 0, 3)
         one_query_rows = _one_query_rows_to_decode_kernel(kv.host_query_lens)
     out = paged_prefill(
         query.squeeze(0).transpose(0, 1), kv.key_pool, kv.value_pool, kv.slot_table, kv.context_lens,

@@ -260,3 +260,25 @@ def test_a_small_pass_runs_one_work_group_per_unit(num_seqs, num_heads, num_kv_h
     first = _run(b, one_query_rows=False)
     assert_within(first, b.oracle(), 2 ** -6, 2e-3)
     assert torch.equal(_run(b, one_query_rows=False), first)
+
+
+@pytest.mark.parametrize("width", [None, 4096])
+def test_a_pass_of_only_one_query_rows_runs_as_a_decode_step(width):
+    """paged_attention over a packed payload whose host query lengths are all 1: the pass is a
+    decode step and runs as one (the same attention as the packed kernels give it)."""
+    from liteinfer_amd.attention import PagedKV, paged_attention
+
+    ctx = [5, 300, 1, 2000, 77]
+    b = PagedBatch(ctx, [1] * len(ctx), dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128,
+                   num_slots=8192, seed=51, width=width)
+    q = b.query.transpose(0, 1).unsqueeze(0)  # [1, heads, tokens, dim], as the model's packed pass holds it
+    kv = PagedKV(b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, query_start_loc=b.query_start_loc,
+                 max_query_len=1, host_context_lens=tuple(ctx), host_query_lens=tuple([1] * len(ctx)))
+    out = paged_attention(q, kv, b.scaling, b.groups)
+    assert out.shape == q.shape
+    want = b.oracle()
+    assert_within(out.squeeze(0).transpose(0, 1), want, 2 ** -6, 2e-3)
+    # without the host lengths the packed kernels serve it: the same attention
+    kv_dev = PagedKV(b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, query_start_loc=b.query_start_loc,
+                     max_query_len=1)
+    assert_within(paged_attention(q, kv_dev, b.scaling, b.groups).squeeze(0).transpose(0, 1), want, 2 ** -6, 2e-3)
