@@ -45,6 +45,16 @@ def test_two_calls_in_a_row_equal_the_workspace_entry_point():
     assert torch.equal(got, want)
 
 
+def test_a_narrow_table_takes_the_short_kernel_through_either_entry_point():
+    print("no-alloc decode: a narrow table (the one-launch short kernel), then a wide one", flush=True)
+    for width in (None, 4096):
+        b = PagedBatch([37, 128, 500, 1000], dtype=torch.bfloat16, num_heads=32, num_kv_heads=8, head_dim=128,
+                       num_slots=8192, seed=9, width=width)
+        want, got = _both(b.query, b.key_pool, b.value_pool, b.slot_table, b.context_lens_t, b.scaling, b.groups)
+        assert torch.equal(got, want)
+        assert_within(got, b.oracle(), 2e-2, 2e-3)
+
+
 @pytest.mark.parametrize("kernel", ["auto", "equal_splits", "generic"])
 def test_every_schedule_meets_the_oracle(kernel):
     print(f"no-alloc decode: kernel={kernel}", flush=True)
